@@ -1,0 +1,51 @@
+"""Public entry point: ``mlc.compile(model, example_inputs, config, device)``.
+
+Reference behaviour followed: ``mlc/api.py:17-53`` (same signature, same pass
+order, and the planner always runs so the unplanned mode still gets its
+alloc/free schedule).
+"""
+
+from __future__ import annotations
+
+from typing import Sequence
+
+import torch
+
+from .config import Config
+from .ir.capture import capture
+from .kernels import Schedule
+from .lower import build_schedule
+from .passes.fusion import plan
+from .passes.memory_planning import plan_memory
+
+
+def compile(model: torch.nn.Module, example_inputs: Sequence[torch.Tensor],
+            config: Config | None = None, device: str | torch.device | None = None):
+    """Compile ``model`` for exactly the shapes of ``example_inputs``.
+
+    The result runs on the MI355X through the HIP backend: fused kernels from
+    hand-written CDNA4 templates, one ``hipMalloc`` arena slab, and the whole
+    schedule replayed as one hipGraph.
+    """
+    from .runtime.executor import CompiledModel
+
+    cfg = config or Config()
+    dev = torch.device(device) if device is not None else _infer_device(example_inputs)
+    graph = capture(model, tuple(example_inputs))
+    schedule = build_pipeline(graph, cfg)
+    return CompiledModel(graph, schedule, cfg, dev)
+
+
+def build_pipeline(graph, cfg: Config) -> Schedule:
+    """Fusion, lowering to kernel IR and memory planning over a captured graph."""
+    groups = plan(graph, cfg)
+    schedule = build_schedule(graph, groups, cfg)
+    plan_memory(graph, schedule, cfg)
+    return schedule
+
+
+def _infer_device(inputs) -> torch.device:
+    for t in inputs:
+        if torch.is_tensor(t):
+            return t.device
+    return torch.device("cpu")

@@ -1,0 +1,944 @@
+"""HIP source generation for gfx950: one ``extern "C" __global__`` function per
+distinct fused kernel, instantiating the hand-written CDNA4 templates in
+``templates/mlc_cdna4.h``.
+
+This replaces the reference's Triton emitters
+(``mlc/codegen/triton_backend.py:206-287``, ``triton_reduction.py:73-274``)
+behind the same seam: it consumes the kernel IR (``PointwiseKernel`` /
+``ReductionKernel``) and returns source plus a launch table. Semantics kept
+from the reference: narrow floats load into fp32 registers, all arithmetic is
+fp32, stores round back to the buffer dtype (round-to-nearest-even); reduce
+identities neutralise masked lanes; row-constant operands are scalar loads.
+
+The MI355X design:
+
+* **pointwise**: one thread per V-element pack (V*itemsize = 16 bytes), so
+  every contiguous operand moves with 128-bit loads/stores; an operand whose
+  index is constant over a pack (a bias broadcast down rows, a row statistic)
+  is one scalar load; anything else is gathered per element. 256-thread
+  workgroups, grid = packs / 256.
+* **persistent reduction**: each row is owned by G lanes (a power of two);
+  lane ``l`` holds columns ``(k*G + l)*V .. +V`` for ``k < K`` in VGPRs, so a
+  row is read once with coalesced 128-bit loads. Rows of <= 64 lanes reduce
+  with DPP/swizzle/readlane inside the wave and several rows share a
+  workgroup; wider rows span whole waves and combine through LDS.
+* **streamed reduction** (rows longer than ``max_persistent_row``): one row
+  per 256-thread workgroup, one chunked pass over HBM per reduce (or one
+  online-softmax pass for max+sum(exp)), then a store pass.
+
+Identical kernel bodies (every transformer layer repeats the same ones) are
+emitted once and shared by name.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+import struct
+from dataclasses import dataclass, field
+
+import torch
+
+from ..config import Config
+from ..ir.scalar import Call, Cast, Const, Expr, Load, Ref, loads as expr_loads, refs as expr_refs
+from ..kernels import Bind, ExternKernel, PointwiseKernel, Reduce, ReductionKernel, Schedule
+from .index import IndexMap
+from .reduction_schedule import plan_passes, scalar_binds, varies_by_column
+
+WAVE = 64
+POINTWISE_BLOCK = 256
+
+#: storage type of each buffer dtype in device code
+STORAGE = {
+    torch.float32: "float",
+    torch.float16: "mlc::f16",
+    torch.bfloat16: "mlc::bf16",
+    torch.float64: "double",
+    torch.int64: "int64_t",
+    torch.int32: "int32_t",
+    torch.int16: "int16_t",
+    torch.int8: "int8_t",
+    torch.uint8: "uint8_t",
+    torch.bool: "bool",
+}
+
+_RANK = {"bool": 0, "int64_t": 1, "float": 2, "double": 3}
+
+
+def compute_type(dtype: torch.dtype) -> str:
+    """Register type a loaded element of ``dtype`` is held in."""
+    if dtype in (torch.float16, torch.bfloat16, torch.float32):
+        return "float"
+    if dtype == torch.float64:
+        return "double"
+    if dtype == torch.bool:
+        return "bool"
+    return "int64_t"
+
+
+def itemsize(dtype: torch.dtype) -> int:
+    return torch.empty((), dtype=dtype).element_size()
+
+
+# --------------------------------------------------------------------------
+# expressions
+# --------------------------------------------------------------------------
+
+def float_literal(v: float) -> str:
+    """The fp32 value of ``v`` as an exact hexadecimal float literal (the
+    oracle also holds literals as fp32 0-dim tensors)."""
+    if v != v:
+        return "__builtin_nanf(\"\")"
+    if v == math.inf:
+        return "__builtin_huge_valf()"
+    if v == -math.inf:
+        return "(-__builtin_huge_valf())"
+    f32 = struct.unpack("<f", struct.pack("<f", float(v)))[0] if abs(v) < 3.5e38 else v
+    if f32 in (math.inf, -math.inf):
+        return "__builtin_huge_valf()" if f32 > 0 else "(-__builtin_huge_valf())"
+    return f"{float(f32).hex()}f"
+
+
+def _round_half(v: float, dtype: torch.dtype) -> float:
+    return float(torch.tensor(v, dtype=dtype).float().item())
+
+
+class Renderer:
+    """Renders scalar expressions to C++ with their register types.
+
+    ``operand(slot)`` and ``temp(name)`` give the C++ expression (and type)
+    that reads an input or a temporary at the current element.
+    """
+
+    def __init__(self, operand, temp) -> None:
+        self.operand = operand
+        self.temp = temp
+
+    def __call__(self, e: Expr) -> tuple[str, str]:
+        if isinstance(e, Load):
+            return self.operand(e.slot)
+        if isinstance(e, Ref):
+            return self.temp(e.name)
+        if isinstance(e, Const):
+            return self.const(e)
+        if isinstance(e, Cast):
+            code, _ = self(e.x)
+            return cast_code(code, e.dtype)
+        if isinstance(e, Call):
+            return self.call(e)
+        raise TypeError(f"cannot emit {type(e).__name__}")
+
+    @staticmethod
+    def const(e: Const) -> tuple[str, str]:
+        v, dt = e.value, e.dtype
+        if isinstance(v, bool) or dt == torch.bool:
+            return ("true" if v else "false"), "bool"
+        if dt in (torch.float16, torch.bfloat16):
+            return float_literal(_round_half(float(v), dt)), "float"
+        if dt in (torch.int64, torch.int32, torch.int16, torch.int8, torch.uint8):
+            return f"((int64_t){int(v)}LL)", "int64_t"
+        if isinstance(v, int) and dt is None:
+            return f"((int64_t){v}LL)", "int64_t"
+        return float_literal(float(v)), "float"
+
+    def call(self, e: Call) -> tuple[str, str]:
+        args = [self(a) for a in e.args]
+        codes = [c for c, _ in args]
+        types = [t for _, t in args]
+        top = max(types, key=lambda t: _RANK[t]) if types else "float"
+        fn = e.fn
+        a = codes[0]
+        if fn in ("add", "sub", "mul"):
+            op = {"add": "+", "sub": "-", "mul": "*"}[fn]
+            t = "int64_t" if top == "bool" else top
+            return f"({a} {op} {codes[1]})", t
+        if fn == "div":
+            if _RANK[top] <= _RANK["int64_t"]:
+                return f"((float)({a}) / (float)({codes[1]}))", "float"
+            return f"({a} / {codes[1]})", top
+        if fn in ("gt", "lt", "ge", "le", "eq", "ne"):
+            op = {"gt": ">", "lt": "<", "ge": ">=", "le": "<=", "eq": "==", "ne": "!="}[fn]
+            return f"({a} {op} {codes[1]})", "bool"
+        if fn == "logical_and":
+            return f"((bool)({a}) && (bool)({codes[1]}))", "bool"
+        if fn == "logical_or":
+            return f"((bool)({a}) || (bool)({codes[1]}))", "bool"
+        if fn == "logical_not":
+            return f"(!({a}))", "bool"
+        if fn == "where":
+            t = max(types[1:], key=lambda x: _RANK[x])
+            return f"(({a}) ? ({t})({codes[1]}) : ({t})({codes[2]}))", t
+        if fn in ("maximum", "minimum"):
+            helper = "max_" if fn == "maximum" else "min_"
+            return f"mlc::{helper}<{top}>(({top})({a}), ({top})({codes[1]}))", top
+        if fn == "pow":
+            t = "double" if top == "double" else "float"
+            return f"mlc::pow_(({t})({a}), ({t})({codes[1]}))", t
+        if fn == "neg":
+            return f"(-({a}))", "int64_t" if types[0] == "bool" else types[0]
+        if fn == "abs":
+            return f"mlc::abs_({a})", types[0]
+        if fn == "floor":
+            return f"mlc::floor_({a})", types[0]
+        if fn == "reciprocal":
+            if types[0] == "double":
+                return f"(1.0 / ({a}))", "double"
+            return f"(1.0f / (float)({a}))", "float"
+        if fn in ("exp", "log", "sqrt", "rsqrt", "sin", "cos", "tanh", "erf", "sigmoid"):
+            t = "double" if types[0] == "double" else "float"
+            arg = a if types[0] in ("float", "double", "int64_t") else f"(float)({a})"
+            return f"mlc::{fn}_({arg})", t
+        raise KeyError(f"no HIP form for scalar function {fn!r}")
+
+
+def cast_code(code: str, dtype: torch.dtype) -> tuple[str, str]:
+    if dtype == torch.float32:
+        return f"((float)({code}))", "float"
+    if dtype == torch.float16:
+        return f"mlc::round_f16((float)({code}))", "float"
+    if dtype == torch.bfloat16:
+        return f"mlc::round_bf16((float)({code}))", "float"
+    if dtype == torch.float64:
+        return f"((double)({code}))", "double"
+    if dtype == torch.bool:
+        return f"(({code}) != 0)", "bool"
+    if dtype == torch.int32:
+        return f"((int64_t)(int32_t)({code}))", "int64_t"
+    return f"((int64_t)({code}))", "int64_t"
+
+
+# --------------------------------------------------------------------------
+# index arithmetic
+# --------------------------------------------------------------------------
+
+def axis_terms(imap: IndexMap, var: str):
+    a = imap.axis(var)
+    return a.terms if a is not None else ()
+
+
+def axis_numel(imap: IndexMap, var: str) -> int:
+    a = imap.axis(var)
+    return a.numel if a is not None else 1
+
+
+def render_terms(terms, numel: int, var: str, it: str) -> list[str]:
+    parts = []
+    for size, ostride, istride in terms:
+        t = var if ostride == 1 else f"({var} / ({it}){ostride})"
+        if size * ostride != numel:
+            t = f"({t} % ({it}){size})"
+        if istride != 1:
+            t = f"{t} * ({it}){istride}"
+        parts.append(t)
+    return parts
+
+
+def join_offset(parts: list[str], it: str) -> str:
+    if not parts:
+        return f"(({it})0)"
+    return "(" + " + ".join(parts) + ")"
+
+
+@dataclass
+class Access:
+    """How one operand is addressed over a V-element run of the fast axis."""
+
+    mode: str  # "uniform" | "affine" | "gather"
+    stride: int = 0
+    aligned: bool = False
+
+
+def classify_access(terms, numel: int, base_terms_is: list[int], base: int, V: int) -> Access:
+    """Access mode of an axis whose packs start at multiples of V.
+
+    ``terms`` are the axis's canonical terms; the run is affine when one term
+    moves with unit iteration stride (and does not wrap inside a pack) and
+    every other term is constant over the pack. ``aligned`` means the run
+    starts on a V-element boundary for every pack, so 128-bit packs apply.
+    """
+    if V == 1:
+        fast = [t for t in terms if t[1] == 1]
+        if not fast:
+            return Access("uniform")
+        return Access("affine", stride=fast[0][2], aligned=False)
+    fast = None
+    for size, ostride, istride in terms:
+        if ostride == 1:
+            if size % V != 0 and size != numel:
+                return Access("gather")
+            fast = (size, ostride, istride)
+        elif ostride % V != 0:
+            return Access("gather")
+    if fast is None:
+        return Access("uniform")
+    others = [t[2] for t in terms if t[1] != 1] + list(base_terms_is)
+    aligned = fast[2] == 1 and base % V == 0 and all(s % V == 0 for s in others)
+    return Access("affine", stride=fast[2], aligned=aligned)
+
+
+def index_type(k) -> str:
+    """32-bit offsets unless some operand's buffer is too large for them."""
+    for a in list(k.inputs) + list(k.outputs):
+        if a.value.buffer.numel >= 2 ** 31:
+            return "uint64_t"
+    return "uint32_t"
+
+
+# --------------------------------------------------------------------------
+# kernel sources
+# --------------------------------------------------------------------------
+
+@dataclass
+class LaunchSpec:
+    """Geometry for one kernel launch; ``symbol`` names the device function."""
+
+    symbol: str
+    grid: int
+    block: int
+    lds_bytes: int = 0
+    meta: dict = field(default_factory=dict)
+
+
+def _params(k) -> list[str]:
+    ps = [f"const {STORAGE[a.dtype]}* __restrict__ in{i}" for i, a in enumerate(k.inputs)]
+    ps += [f"{STORAGE[a.dtype]}* __restrict__ out{i}" for i, a in enumerate(k.outputs)]
+    return ps
+
+
+def _vec_width(dtypes) -> int:
+    sizes = [itemsize(d) for d in dtypes]
+    return max(1, 16 // min(sizes)) if sizes else 1
+
+
+def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, LaunchSpec]:
+    """Source (with the placeholder name ``KERNEL``) and launch spec."""
+    N = k.numel
+    it = index_type(k)
+    V = _vec_width([a.dtype for a in k.inputs] + [a.dtype for a in k.outputs])
+    while V > 1 and N < V:
+        V //= 2
+
+    accesses = []
+    for a in k.inputs:
+        terms = axis_terms(a.index, "idx")
+        accesses.append(classify_access(terms, N, [], a.index.base, V))
+    out_access = []
+    for a in k.outputs:
+        terms = axis_terms(a.index, "idx")
+        out_access.append(classify_access(terms, N, [], a.index.base, V))
+
+    def offset(a, var: str) -> str:
+        parts = render_terms(axis_terms(a.index, "idx"), N, var, it)
+        if a.index.base:
+            parts.append(f"({it}){a.index.base}")
+        return join_offset(parts, it)
+
+    in_types = [compute_type(a.dtype) for a in k.inputs]
+    temp_types: dict[str, str] = {}
+    L: list[str] = []
+    L.append(f"extern \"C\" __global__ void __launch_bounds__({POINTWISE_BLOCK}) "
+             f"KERNEL({', '.join(_params(k))}) {{")
+    L.append(f"  // pointwise over {list(k.space)} = {N} elements, {V}-element packs")
+    L.append(f"  constexpr {it} N = ({it}){N};")
+    L.append(f"  constexpr int V = {V};")
+    L.append(f"  const {it} e0 = (({it})blockIdx.x * {POINTWISE_BLOCK} + threadIdx.x) * V;")
+    L.append("  if (e0 >= N) return;")
+
+    def body_lines(ref_in, indent: str) -> list[str]:
+        lines = []
+        r = Renderer(ref_in, lambda n: (n, temp_types[n]))
+        for name, expr in k.body:
+            code, t = r(expr)
+            temp_types[name] = t
+            lines.append(f"{indent}const {t} {name} = {code};")
+        return lines, r
+
+    # -- vector path --
+    vec: list[str] = []
+    for i, (a, acc) in enumerate(zip(k.inputs, accesses)):
+        ct = in_types[i]
+        if acc.mode == "uniform":
+            vec.append(f"    const {ct} v{i} = mlc::ld(in{i} + {offset(a, 'e0')});")
+        elif acc.mode == "affine" and acc.aligned:
+            vec.append(f"    {ct} v{i}[V]; mlc::load_pack<V>(v{i}, in{i} + {offset(a, 'e0')});")
+        elif acc.mode == "affine":
+            vec.append(f"    {ct} v{i}[V];")
+            vec.append(f"    {{ const {it} o = {offset(a, 'e0')};")
+            vec.append("#pragma unroll")
+            vec.append(f"      for (int j = 0; j < V; ++j) v{i}[j] = mlc::ld(in{i} + o + ({it})j * ({it}){acc.stride}); }}")
+        else:
+            vec.append(f"    {ct} v{i}[V];")
+            vec.append("#pragma unroll")
+            vec.append(f"    for (int j = 0; j < V; ++j) v{i}[j] = mlc::ld(in{i} + {offset(a, '(e0 + (' + it + ')j)')});")
+
+    def ref_vec(slot):
+        mode = accesses[slot].mode
+        return (f"v{slot}" if mode == "uniform" else f"v{slot}[j]"), in_types[slot]
+
+    out_vals = []
+    for i, a in enumerate(k.outputs):
+        vec.append(f"    {compute_type_of_out(k, a)} o{i}[V];")
+    vec.append("#pragma unroll")
+    vec.append("    for (int j = 0; j < V; ++j) {")
+    blines, r = body_lines(ref_vec, "      ")
+    vec += blines
+    for i, a in enumerate(k.outputs):
+        code, _ = r(k.out_expr[a.value.name])
+        vec.append(f"      o{i}[j] = {code};")
+    vec.append("    }")
+    for i, (a, acc) in enumerate(zip(k.outputs, out_access)):
+        if acc.mode == "affine" and acc.aligned:
+            vec.append(f"    mlc::store_pack<V>(out{i} + {offset(a, 'e0')}, o{i});")
+        else:
+            vec.append("#pragma unroll")
+            vec.append(f"    for (int j = 0; j < V; ++j) mlc::st(out{i} + {offset(a, '(e0 + (' + it + ')j)')}, o{i}[j]);")
+
+    exact = N % V == 0
+    if exact:
+        L.append("  {")
+        L += vec
+        L.append("  }")
+    else:
+        L.append("  if (e0 + V <= N) {")
+        L += vec
+        L.append("  } else {")
+        L.append(f"    for ({it} e = e0; e < N; ++e) {{")
+        for i, a in enumerate(k.inputs):
+            L.append(f"      const {in_types[i]} s{i} = mlc::ld(in{i} + {offset(a, 'e')});")
+        temp_types.clear()
+        blines, r = body_lines(lambda s: (f"s{s}", in_types[s]), "      ")
+        L += blines
+        for i, a in enumerate(k.outputs):
+            code, _ = r(k.out_expr[a.value.name])
+            L.append(f"      mlc::st(out{i} + {offset(a, 'e')}, {code});")
+        L.append("    }")
+        L.append("  }")
+    L.append("}")
+
+    packs = -(-N // V)
+    grid = max(1, -(-packs // POINTWISE_BLOCK))
+    spec = LaunchSpec("", grid, POINTWISE_BLOCK, 0,
+                      {"kind": "pointwise", "vec": V, "numel": N,
+                       "access": [a.mode + ("+aligned" if a.aligned else "") for a in accesses]})
+    return "\n".join(L), spec
+
+
+def compute_type_of_out(k, a) -> str:
+    """Register type of an output's stored expression."""
+    e = k.out_expr[a.value.name]
+    temp_types: dict[str, str] = {}
+    if isinstance(k, PointwiseKernel):
+        for name, expr in k.body:
+            temp_types[name] = _type_only(expr, k, temp_types)
+    else:
+        for s in k.steps:
+            temp_types[s.name] = _type_only(s.expr, k, temp_types)
+    return _type_only(e, k, temp_types)
+
+
+def _type_only(e: Expr, k, temp_types) -> str:
+    r = Renderer(lambda s: ("x", compute_type(k.inputs[s].dtype)), lambda n: ("x", temp_types[n]))
+    return r(e)[1]
+
+
+# --------------------------------------------------------------------------
+# persistent reductions
+# --------------------------------------------------------------------------
+
+_IDENTITY = {
+    "sum": {"float": "0.0f", "double": "0.0", "int64_t": "((int64_t)0)"},
+    "prod": {"float": "1.0f", "double": "1.0", "int64_t": "((int64_t)1)"},
+    "max": {"float": "(-__builtin_huge_valf())", "double": "(-__builtin_huge_val())",
+            "int64_t": "INT64_MIN"},
+    "min": {"float": "__builtin_huge_valf()", "double": "__builtin_huge_val()",
+            "int64_t": "INT64_MAX"},
+}
+_OP = {"sum": "mlc::OpSum", "prod": "mlc::OpProd", "max": "mlc::OpMax", "min": "mlc::OpMin"}
+
+
+def _prev_pow2(n: int) -> int:
+    return 1 << (max(1, n).bit_length() - 1)
+
+
+def reduction_geometry(n_rows: int, n_cols: int, V: int) -> dict:
+    """Lanes per row G, packs per lane K, rows per workgroup."""
+    nvec = -(-n_cols // V)
+    G = None
+    if nvec <= WAVE * 8:
+        for g in (64, 32, 16, 8, 4, 2, 1):
+            if g <= nvec and nvec % g == 0 and nvec // g <= 8:
+                G = g
+                break
+        if G is None:
+            G = min(WAVE, _prev_pow2(nvec))
+    else:
+        G = 128
+        while G < 1024 and -(-nvec // G) > 8:
+            G *= 2
+    K = -(-nvec // G)
+    if G <= WAVE:
+        rows = max(WAVE // G, min(256 // G, max(1, -(-n_rows // 1024))))
+        rows = 1 << (rows.bit_length() - 1) if rows & (rows - 1) else rows
+    else:
+        rows = 1
+    return {"G": G, "K": K, "rows_per_wg": rows, "block": G * rows, "nvec": nvec}
+
+
+def _row_col_access(k: ReductionKernel, a, V: int) -> Access:
+    C = k.reduce_numel
+    col = axis_terms(a.index, "col")
+    row_is = [t[2] for t in axis_terms(a.index, "row")]
+    return classify_access(col, C, row_is, a.index.base, V)
+
+
+def _choose_reduction_vec(k: ReductionKernel) -> int:
+    C = k.reduce_numel
+    col_args = [a for a in k.inputs if a.index.varies_along("col")]
+    col_args += [a for a in k.outputs if a.value.name not in k.row_outputs]
+    V = _vec_width([a.dtype for a in col_args]) if col_args else 1
+    while V > 1:
+        if C % V == 0 and all(_row_col_access(k, a, V).mode != "gather" for a in col_args):
+            break
+        V //= 2
+    return V
+
+
+class _RowOffsets:
+    def __init__(self, k: ReductionKernel, it: str) -> None:
+        self.k = k
+        self.it = it
+
+    def row(self, a, var: str = "row") -> str:
+        parts = render_terms(axis_terms(a.index, "row"), axis_numel(a.index, "row"), var, self.it)
+        if a.index.base:
+            parts.append(f"({self.it}){a.index.base}")
+        return join_offset(parts, self.it)
+
+    def col(self, a, var: str) -> str:
+        return join_offset(render_terms(axis_terms(a.index, "col"), self.k.reduce_numel, var,
+                                        self.it), self.it)
+
+
+def emit_reduction(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
+    if k.two_pass:
+        return emit_streamed(k, cfg)
+    return emit_persistent(k, cfg)
+
+
+def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
+    R, C = k.n_rows, k.reduce_numel
+    it = index_type(k)
+    V = _choose_reduction_vec(k)
+    geo = reduction_geometry(R, C, V)
+    G, K, RPW, WG = geo["G"], geo["K"], geo["rows_per_wg"], geo["block"]
+    exact = C == G * K * V
+    offs = _RowOffsets(k, it)
+    col_slots = [i for i, a in enumerate(k.inputs) if a.index.varies_along("col")]
+    vector = varies_by_column(k)
+    in_types = [compute_type(a.dtype) for a in k.inputs]
+    temp_types: dict[str, str] = {}
+
+    L: list[str] = []
+    L.append(f"extern \"C\" __global__ void __launch_bounds__({WG}) "
+             f"KERNEL({', '.join(_params(k))}) {{")
+    L.append(f"  // persistent: {R} rows of {C}; {G} lanes x {K} packs x {V} per row, "
+             f"{RPW} rows per workgroup")
+    L.append(f"  constexpr {it} R = ({it}){R};")
+    L.append(f"  constexpr {it} C = ({it}){C};")
+    L.append(f"  constexpr int G = {G}, K = {K}, V = {V};")
+    lds = 0
+    if G > WAVE:
+        for s in k.reduces:
+            t = _type_only(s.expr, k, _step_types(k))
+            L.append(f"  __shared__ {t} lds_{s.name}[G / 64];")
+            lds += (G // WAVE) * {"float": 4, "double": 8, "int64_t": 8, "bool": 4}[t]
+    L.append(f"  const {it} row = ({it})blockIdx.x * {RPW} + threadIdx.x / G;")
+    L.append(f"  const {it} lane = threadIdx.x % G;")
+    if R % RPW != 0:
+        L.append("  if (row >= R) return;")
+    if not exact:
+        L.append("  bool valid[K];")
+        L.append("#pragma unroll")
+        L.append(f"  for (int p = 0; p < K; ++p) valid[p] = (({it})p * G + lane) * V < C;")
+
+    # operands
+    for i, a in enumerate(k.inputs):
+        ct = in_types[i]
+        if i not in col_slots:
+            L.append(f"  const {ct} v{i} = mlc::ld(in{i} + {offs.row(a)});")
+            continue
+        acc = _row_col_access(k, a, V)
+        L.append(f"  {ct} v{i}[K][V];")
+        L.append(f"  {{ const {it} rb = {offs.row(a)};")
+        L.append("#pragma unroll")
+        L.append("    for (int p = 0; p < K; ++p) {")
+        L.append(f"      const {it} c0 = (({it})p * G + lane) * V;")
+        guard = "" if exact else "if (valid[p]) "
+        if not exact:
+            L.append("      if (!valid[p]) {")
+            L.append("#pragma unroll")
+            L.append(f"        for (int j = 0; j < V; ++j) v{i}[p][j] = ({ct})0;")
+            L.append("        continue;")
+            L.append("      }")
+        if acc.mode == "affine" and acc.aligned:
+            L.append(f"      mlc::load_pack<V>(v{i}[p], in{i} + rb + {offs.col(a, 'c0')});")
+        elif acc.mode == "affine":
+            L.append(f"      const {it} o = rb + {offs.col(a, 'c0')};")
+            L.append("#pragma unroll")
+            L.append(f"      for (int j = 0; j < V; ++j) v{i}[p][j] = mlc::ld(in{i} + o + ({it})j * ({it}){acc.stride});")
+        else:
+            L.append("#pragma unroll")
+            L.append(f"      for (int j = 0; j < V; ++j) v{i}[p][j] = mlc::ld(in{i} + rb + {offs.col(a, '(c0 + (' + it + ')j)')});")
+        L.append("    }")
+        L.append("  }")
+        del guard
+
+    def ref_elem(slot):
+        if slot in col_slots:
+            return f"v{slot}[p][j]", in_types[slot]
+        return f"v{slot}", in_types[slot]
+
+    def ref_scalar(slot):
+        if slot in col_slots:
+            raise AssertionError("column operand read in a row-scalar expression")
+        return f"v{slot}", in_types[slot]
+
+    def temp_elem(name):
+        return (f"{name}[p][j]" if name in vector else name), temp_types[name]
+
+    def temp_scalar(name):
+        if name in vector:
+            raise AssertionError("vector temp read in a row-scalar expression")
+        return name, temp_types[name]
+
+    elem_r = Renderer(ref_elem, temp_elem)
+    scal_r = Renderer(ref_scalar, temp_scalar)
+
+    for s in k.steps:
+        if isinstance(s, Bind):
+            if s.name in vector:
+                code, t = elem_r(s.expr)
+                temp_types[s.name] = t
+                L.append(f"  {t} {s.name}[K][V];")
+                L.append("#pragma unroll")
+                L.append("  for (int p = 0; p < K; ++p)")
+                L.append("#pragma unroll")
+                L.append("    for (int j = 0; j < V; ++j)")
+                L.append(f"      {s.name}[p][j] = {code};")
+            else:
+                code, t = scal_r(s.expr)
+                temp_types[s.name] = t
+                L.append(f"  const {t} {s.name} = {code};")
+            continue
+        # Reduce
+        code, t = elem_r(s.expr)
+        if t == "bool":
+            code, t = f"((int64_t)({code}))", "int64_t"
+        temp_types[s.name] = t
+        ident = _IDENTITY[s.kind][t]
+        op = _OP[s.kind]
+        varies = _expr_varies(s.expr, col_slots, vector)
+        L.append(f"  {t} {s.name};")
+        L.append("  {")
+        if varies:
+            L.append(f"    {t} acc = {ident};")
+            L.append("#pragma unroll")
+            L.append("    for (int p = 0; p < K; ++p) {")
+            if not exact:
+                L.append("      if (!valid[p]) continue;")
+            L.append("#pragma unroll")
+            L.append(f"      for (int j = 0; j < V; ++j) acc = {op}::f(acc, ({t})({code}));")
+            L.append("    }")
+        else:
+            # constant along the row: every valid element contributes the same value
+            scode, _ = scal_r(s.expr)
+            L.append(f"    {t} acc = {ident};")
+            L.append(f"    const {t} x = ({t})({scode});")
+            L.append("#pragma unroll")
+            L.append("    for (int p = 0; p < K; ++p) {")
+            if not exact:
+                L.append("      if (!valid[p]) continue;")
+            L.append(f"      for (int j = 0; j < V; ++j) acc = {op}::f(acc, x);")
+            L.append("    }")
+        slot = f"lds_{s.name}" if G > WAVE else "nullptr"
+        L.append(f"    {s.name} = mlc::row_reduce<G, {op}>(acc, ({t}*){slot});")
+        L.append("  }")
+
+    # element stores
+    for i, a in enumerate(k.outputs):
+        nm = a.value.name
+        if nm in k.row_outputs:
+            continue
+        e = k.out_expr[nm]
+        acc = _row_col_access(k, a, V)
+        ot = compute_type_of_out(k, a)
+        L.append(f"  {{ // store {nm}")
+        L.append(f"    const {it} rb = {offs.row(a)};")
+        L.append("#pragma unroll")
+        L.append("    for (int p = 0; p < K; ++p) {")
+        if not exact:
+            L.append("      if (!valid[p]) continue;")
+        L.append(f"      const {it} c0 = (({it})p * G + lane) * V;")
+        if _expr_varies(e, col_slots, vector):
+            code, _ = elem_r(e)
+        else:
+            code, _ = scal_r(e)
+        L.append(f"      {ot} o[V];")
+        L.append("#pragma unroll")
+        L.append(f"      for (int j = 0; j < V; ++j) o[j] = {code};")
+        if acc.mode == "affine" and acc.aligned:
+            L.append(f"      mlc::store_pack<V>(out{i} + rb + {offs.col(a, 'c0')}, o);")
+        else:
+            L.append("#pragma unroll")
+            L.append(f"      for (int j = 0; j < V; ++j) mlc::st(out{i} + rb + {offs.col(a, '(c0 + (' + it + ')j)')}, o[j]);")
+        L.append("    }")
+        L.append("  }")
+
+    # row stores
+    row_store = [(i, a) for i, a in enumerate(k.outputs) if a.value.name in k.row_outputs]
+    if row_store:
+        L.append("  if (lane == 0) {")
+        for i, a in row_store:
+            code, _ = scal_r(k.out_expr[a.value.name])
+            L.append(f"    mlc::st(out{i} + {offs.row(a)}, {code});")
+        L.append("  }")
+    L.append("}")
+
+    grid = -(-R // RPW)
+    spec = LaunchSpec("", grid, WG, lds, {"kind": "reduction", "mode": "persistent", "vec": V,
+                                          "lanes_per_row": G, "packs": K, "rows_per_wg": RPW,
+                                          "rows": R, "cols": C})
+    return "\n".join(L), spec
+
+
+def _step_types(k: ReductionKernel) -> dict[str, str]:
+    types: dict[str, str] = {}
+    for s in k.steps:
+        t = _type_only(s.expr, k, types)
+        if isinstance(s, Reduce) and t == "bool":
+            t = "int64_t"
+        types[s.name] = t
+    return types
+
+
+def _expr_varies(e: Expr, col_slots, vector) -> bool:
+    return bool(expr_loads(e) & set(col_slots)) or bool(expr_refs(e) & set(vector))
+
+
+# --------------------------------------------------------------------------
+# streamed reductions
+# --------------------------------------------------------------------------
+
+STREAM_BLOCK = 256
+
+
+def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
+    """One row per workgroup; each pass of the reduction schedule streams the
+    row from HBM in chunks of ``STREAM_BLOCK * V`` elements."""
+    R, C = k.n_rows, k.reduce_numel
+    it = index_type(k)
+    V = _choose_reduction_vec(k)
+    G = STREAM_BLOCK
+    while G > WAVE and G * V > max(C, WAVE * V):
+        G //= 2
+    offs = _RowOffsets(k, it)
+    col_slots = [i for i, a in enumerate(k.inputs) if a.index.varies_along("col")]
+    vector = varies_by_column(k)
+    scalars = {b.name for b in scalar_binds(k)}
+    passes = plan_passes(k)
+    in_types = [compute_type(a.dtype) for a in k.inputs]
+    temp_types = _step_types(k)
+    chunk_exact = C % (G * V) == 0
+
+    L: list[str] = []
+    L.append(f"extern \"C\" __global__ void __launch_bounds__({G}) "
+             f"KERNEL({', '.join(_params(k))}) {{")
+    L.append(f"  // streamed: {R} rows of {C}, {len(passes)} passes, chunks of {G} lanes x {V}")
+    L.append(f"  constexpr {it} C = ({it}){C};")
+    L.append(f"  constexpr int G = {G}, V = {V};")
+    lds = 0
+    need_lds = G > WAVE
+    if need_lds:
+        for p_i, p in enumerate(passes):
+            for r in p.reduces:
+                t = temp_types[r.name]
+                L.append(f"  __shared__ {t} lds_{r.name}[G / 64];")
+                lds += (G // WAVE) * (8 if t in ("double", "int64_t") else 4)
+            if p.online_softmax is not None:
+                L.append(f"  __shared__ float lds_w_{p.online_softmax.sum_step.name}[G / 64];")
+                lds += (G // WAVE) * 4
+    L.append(f"  const {it} row = ({it})blockIdx.x;")
+    L.append(f"  const {it} lane = threadIdx.x;")
+    for i, a in enumerate(k.inputs):
+        if i not in col_slots:
+            L.append(f"  const {in_types[i]} v{i} = mlc::ld(in{i} + {offs.row(a)});")
+
+    def ref_elem(slot):
+        if slot in col_slots:
+            return f"v{slot}[j]", in_types[slot]
+        return f"v{slot}", in_types[slot]
+
+    def temp_elem(name):
+        return (f"{name}[j]" if name in vector else name), temp_types[name]
+
+    def temp_scalar(name):
+        return name, temp_types[name]
+
+    elem_r = Renderer(ref_elem, temp_elem)
+    scal_r = Renderer(lambda s: (f"v{s}", in_types[s]), temp_scalar)
+
+    def slots_for(p) -> list[int]:
+        used: set[int] = set()
+        for b in p.binds:
+            used |= expr_loads(b.expr)
+        for r in p.reduces:
+            used |= expr_loads(r.expr)
+        if p.online_softmax is not None:
+            used |= expr_loads(p.online_softmax.value)
+        for nm in p.stores:
+            used |= expr_loads(k.out_expr[nm])
+        return sorted(used & set(col_slots))
+
+    def emit_pass(p) -> list[str]:
+        out: list[str] = []
+        online = p.online_softmax
+        if online is not None:
+            out.append("  float m_run = (-__builtin_huge_valf()), l_run = 0.0f;")
+        for r in p.reduces if online is None else []:
+            t = temp_types[r.name]
+            out.append(f"  {t} acc_{r.name} = {_IDENTITY[r.kind][t]};")
+        out.append(f"  for ({it} base = 0; base < C; base += ({it})G * V) {{")
+        out.append(f"    const {it} c0 = base + lane * V;")
+        if not chunk_exact:
+            out.append("    if (c0 >= C) continue;")
+        for i in slots_for(p):
+            a = k.inputs[i]
+            acc = _row_col_access(k, a, V)
+            ct = in_types[i]
+            out.append(f"    {ct} v{i}[V];")
+            if acc.mode == "affine" and acc.aligned:
+                out.append(f"    mlc::load_pack<V>(v{i}, in{i} + {offs.row(a)} + {offs.col(a, 'c0')});")
+            else:
+                out.append("#pragma unroll")
+                out.append(f"    for (int j = 0; j < V; ++j) v{i}[j] = mlc::ld(in{i} + {offs.row(a)} + {offs.col(a, '(c0 + (' + it + ')j)')});")
+        for b in p.binds:
+            code, t = elem_r(b.expr)
+            out.append(f"    {t} {b.name}[V];")
+            out.append("#pragma unroll")
+            out.append(f"    for (int j = 0; j < V; ++j) {b.name}[j] = {code};")
+        if online is not None:
+            code, _ = elem_r(online.value)
+            out.append("#pragma unroll")
+            out.append("    for (int j = 0; j < V; ++j) {")
+            out.append(f"      const float x = (float)({code});")
+            out.append("      const float m_new = mlc::max_<float>(m_run, x);")
+            out.append("      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : mlc::exp_(m_run - m_new);")
+            out.append("      l_run = l_run * alpha + mlc::exp_(x - m_new);")
+            out.append("      m_run = m_new;")
+            out.append("    }")
+        else:
+            for r in p.reduces:
+                code, t = elem_r(r.expr)
+                out.append("#pragma unroll")
+                out.append(f"    for (int j = 0; j < V; ++j) acc_{r.name} = {_OP[r.kind]}::f(acc_{r.name}, ({t})({code}));")
+        for nm in p.stores:
+            i = next(ii for ii, a in enumerate(k.outputs) if a.value.name == nm)
+            a = k.outputs[i]
+            acc = _row_col_access(k, a, V)
+            ot = compute_type_of_out(k, a)
+            e = k.out_expr[nm]
+            code, _ = (elem_r(e) if _expr_varies(e, col_slots, vector) else scal_r(e))
+            out.append(f"    {{ {ot} o[V];")
+            out.append("#pragma unroll")
+            out.append(f"      for (int j = 0; j < V; ++j) o[j] = {code};")
+            if acc.mode == "affine" and acc.aligned:
+                out.append(f"      mlc::store_pack<V>(out{i} + {offs.row(a)} + {offs.col(a, 'c0')}, o); }}")
+            else:
+                out.append("#pragma unroll")
+                out.append(f"      for (int j = 0; j < V; ++j) mlc::st(out{i} + {offs.row(a)} + {offs.col(a, '(c0 + (' + it + ')j)')}, o[j]); }}")
+        out.append("  }")
+        if online is not None:
+            mx, sm = online.max_step.name, online.sum_step.name
+            slot = f"lds_{mx}" if need_lds else "nullptr"
+            out.append(f"  const float {mx} = mlc::row_reduce<G, mlc::OpMax>(m_run, (float*){slot});")
+            out.append(f"  const float w_{sm} = (m_run == (-__builtin_huge_valf())) ? 0.0f : mlc::exp_(m_run - {mx});")
+            slot = f"lds_{sm}" if need_lds else "nullptr"
+            out.append(f"  const float {sm} = mlc::row_reduce<G, mlc::OpSum>(l_run * w_{sm}, (float*){slot});")
+        else:
+            for r in p.reduces:
+                t = temp_types[r.name]
+                slot = f"lds_{r.name}" if need_lds else "nullptr"
+                out.append(f"  const {t} {r.name} = mlc::row_reduce<G, {_OP[r.kind]}>(acc_{r.name}, ({t}*){slot});")
+        return out
+
+    owner = {r.name: p for p in passes for r in p.reduces}
+    emitted: set[int] = set()
+    for s in k.steps:
+        if isinstance(s, Reduce):
+            p = owner[s.name]
+            if id(p) in emitted:
+                continue
+            emitted.add(id(p))
+            L.append("  {" if False else "")
+            L += emit_pass(p)
+        elif s.name in scalars:
+            code, t = scal_r(s.expr)
+            L.append(f"  const {t} {s.name} = {code};")
+    for p in passes:
+        if p.stores and not p.reduces:
+            L += emit_pass(p)
+    row_store = [(i, a) for i, a in enumerate(k.outputs) if a.value.name in k.row_outputs]
+    if row_store:
+        L.append("  if (lane == 0) {")
+        for i, a in row_store:
+            code, _ = scal_r(k.out_expr[a.value.name])
+            L.append(f"    mlc::st(out{i} + {offs.row(a)}, {code});")
+        L.append("  }")
+    L.append("}")
+    spec = LaunchSpec("", R, G, lds, {"kind": "reduction", "mode": "streamed", "vec": V,
+                                      "lanes_per_row": G, "passes": len(passes),
+                                      "rows": R, "cols": C})
+    return "\n".join([x for x in L if x != ""]), spec
+
+
+# --------------------------------------------------------------------------
+# module
+# --------------------------------------------------------------------------
+
+PRELUDE = """// Generated by mlc's HIP backend for gfx950. One function per distinct fused
+// kernel; the launch table lives on the host side.
+#include "mlc_cdna4.h"
+"""
+
+
+@dataclass
+class Module:
+    source: str
+    launches: dict[str, LaunchSpec]
+    #: symbol -> kernel body (for inspection)
+    functions: dict[str, str]
+
+
+def emit_kernel(k, cfg: Config) -> tuple[str, LaunchSpec]:
+    if isinstance(k, PointwiseKernel):
+        return emit_pointwise(k, cfg)
+    if isinstance(k, ReductionKernel):
+        return emit_reduction(k, cfg)
+    raise TypeError(f"no HIP emitter for {type(k).__name__}")
+
+
+def generate_module(schedule: Schedule, cfg: Config) -> Module:
+    """Every generated kernel of ``schedule`` as one HIP translation unit."""
+    functions: dict[str, str] = {}
+    launches: dict[str, LaunchSpec] = {}
+    for k in schedule.kernels:
+        if isinstance(k, ExternKernel):
+            continue
+        body, spec = emit_kernel(k, cfg)
+        digest = hashlib.sha256(body.encode()).hexdigest()[:16]
+        symbol = f"mlc_{digest}"
+        functions.setdefault(symbol, body.replace("KERNEL(", f"{symbol}(", 1))
+        spec.symbol = symbol
+        launches[k.name] = spec
+    parts = [PRELUDE] + [functions[s] for s in sorted(functions)]
+    return Module("\n\n".join(parts) + "\n", launches, functions)

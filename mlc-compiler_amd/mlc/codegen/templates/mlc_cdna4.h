@@ -1,0 +1,257 @@
+// Hand-written CDNA4 (gfx950) device templates instantiated by every fused
+// kernel the HIP backend generates.
+//
+//  * 128-bit coalesced global loads/stores of fp16/bf16/fp32 packs
+//    (load_pack / store_pack), converted to fp32 registers on load and back
+//    with round-to-nearest-even on store;
+//  * the pointwise driver: one thread per V-element pack over a flat space;
+//  * wave64 cross-lane reductions for groups of 2..64 lanes using DPP
+//    (quad_perm, row_half_mirror, row_mirror), ds_swizzle (xor 16 within a
+//    32-lane half) and v_readlane (the two 32-lane halves), giving every lane
+//    of the group the bit-identical result; groups wider than a wave combine
+//    per-wave partials through LDS in a fixed order;
+//  * scalar math helpers with torch semantics (NaN-propagating max/min, IEEE
+//    division, integer true division).
+//
+// No MFMA: every kernel generated here is HBM-bandwidth bound.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlc {
+
+typedef _Float16 f16;
+
+// ---------------------------------------------------------------------------
+// storage <-> register conversion
+// ---------------------------------------------------------------------------
+struct bf16 {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float ld(const float* p) { return *p; }
+__device__ __forceinline__ float ld(const f16* p) { return static_cast<float>(*p); }
+__device__ __forceinline__ float ld(const bf16* p) { return bf16_to_f32(p->bits); }
+__device__ __forceinline__ double ld(const double* p) { return *p; }
+__device__ __forceinline__ int64_t ld(const int64_t* p) { return *p; }
+__device__ __forceinline__ int64_t ld(const int32_t* p) { return *p; }
+__device__ __forceinline__ int64_t ld(const int16_t* p) { return *p; }
+__device__ __forceinline__ int64_t ld(const int8_t* p) { return *p; }
+__device__ __forceinline__ int64_t ld(const uint8_t* p) { return *p; }
+__device__ __forceinline__ bool ld(const bool* p) { return *reinterpret_cast<const uint8_t*>(p) != 0; }
+
+template <class S, class X> __device__ __forceinline__ S cvt(X x) { return static_cast<S>(x); }
+template <> __device__ __forceinline__ f16 cvt<f16, float>(float x) { return static_cast<f16>(x); }
+template <> __device__ __forceinline__ f16 cvt<f16, double>(double x) { return static_cast<f16>(static_cast<float>(x)); }
+template <> __device__ __forceinline__ bf16 cvt<bf16, float>(float x) { return bf16{f32_to_bf16(x)}; }
+template <> __device__ __forceinline__ bf16 cvt<bf16, double>(double x) { return bf16{f32_to_bf16(static_cast<float>(x))}; }
+template <> __device__ __forceinline__ bf16 cvt<bf16, int64_t>(int64_t x) { return bf16{f32_to_bf16(static_cast<float>(x))}; }
+template <> __device__ __forceinline__ bf16 cvt<bf16, bool>(bool x) { return bf16{f32_to_bf16(x ? 1.0f : 0.0f)}; }
+template <> __device__ __forceinline__ bool cvt<bool, float>(float x) { return x != 0.0f; }
+template <> __device__ __forceinline__ bool cvt<bool, double>(double x) { return x != 0.0; }
+template <> __device__ __forceinline__ bool cvt<bool, int64_t>(int64_t x) { return x != 0; }
+
+template <class S, class X> __device__ __forceinline__ void st(S* p, X x) { *p = cvt<S>(x); }
+
+// value rounded through a narrow float type, as a cast inside a kernel body
+__device__ __forceinline__ float round_f16(float x) { return static_cast<float>(static_cast<f16>(x)); }
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// ---------------------------------------------------------------------------
+// 128-bit packs
+// ---------------------------------------------------------------------------
+template <class S, int V> struct alignas(sizeof(S) * V) pack {
+  S x[V];
+};
+
+// V contiguous elements starting at an address aligned to V*sizeof(S).
+template <int V, class S, class R>
+__device__ __forceinline__ void load_pack(R (&dst)[V], const S* __restrict__ p) {
+  if constexpr (sizeof(S) * V > 16) {
+    constexpr int H = 16 / sizeof(S);
+    static_assert(V % H == 0, "pack split");
+#pragma unroll
+    for (int h = 0; h < V / H; ++h) {
+      const pack<S, H> w = *reinterpret_cast<const pack<S, H>*>(p + h * H);
+#pragma unroll
+      for (int i = 0; i < H; ++i) dst[h * H + i] = ld(&w.x[i]);
+    }
+  } else {
+    const pack<S, V> w = *reinterpret_cast<const pack<S, V>*>(p);
+#pragma unroll
+    for (int i = 0; i < V; ++i) dst[i] = ld(&w.x[i]);
+  }
+}
+
+template <int V, class S, class R>
+__device__ __forceinline__ void store_pack(S* __restrict__ p, const R (&src)[V]) {
+  if constexpr (sizeof(S) * V > 16) {
+    constexpr int H = 16 / sizeof(S);
+#pragma unroll
+    for (int h = 0; h < V / H; ++h) {
+      pack<S, H> w;
+#pragma unroll
+      for (int i = 0; i < H; ++i) w.x[i] = cvt<S>(src[h * H + i]);
+      *reinterpret_cast<pack<S, H>*>(p + h * H) = w;
+    }
+  } else {
+    pack<S, V> w;
+#pragma unroll
+    for (int i = 0; i < V; ++i) w.x[i] = cvt<S>(src[i]);
+    *reinterpret_cast<pack<S, V>*>(p) = w;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// scalar math with torch semantics
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float exp_(float x) { return expf(x); }
+__device__ __forceinline__ double exp_(double x) { return exp(x); }
+__device__ __forceinline__ float log_(float x) { return logf(x); }
+__device__ __forceinline__ double log_(double x) { return log(x); }
+__device__ __forceinline__ float sqrt_(float x) { return sqrtf(x); }
+__device__ __forceinline__ double sqrt_(double x) { return sqrt(x); }
+__device__ __forceinline__ float rsqrt_(float x) { return 1.0f / sqrtf(x); }
+__device__ __forceinline__ double rsqrt_(double x) { return 1.0 / sqrt(x); }
+__device__ __forceinline__ float sin_(float x) { return sinf(x); }
+__device__ __forceinline__ double sin_(double x) { return sin(x); }
+__device__ __forceinline__ float cos_(float x) { return cosf(x); }
+__device__ __forceinline__ double cos_(double x) { return cos(x); }
+__device__ __forceinline__ float tanh_(float x) { return tanhf(x); }
+__device__ __forceinline__ double tanh_(double x) { return tanh(x); }
+__device__ __forceinline__ float erf_(float x) { return erff(x); }
+__device__ __forceinline__ double erf_(double x) { return erf(x); }
+__device__ __forceinline__ float sigmoid_(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ double sigmoid_(double x) { return 1.0 / (1.0 + exp(-x)); }
+__device__ __forceinline__ float floor_(float x) { return floorf(x); }
+__device__ __forceinline__ double floor_(double x) { return floor(x); }
+__device__ __forceinline__ int64_t floor_(int64_t x) { return x; }
+__device__ __forceinline__ float abs_(float x) { return fabsf(x); }
+__device__ __forceinline__ double abs_(double x) { return fabs(x); }
+__device__ __forceinline__ int64_t abs_(int64_t x) { return x < 0 ? -x : x; }
+__device__ __forceinline__ float pow_(float a, float b) { return powf(a, b); }
+__device__ __forceinline__ double pow_(double a, double b) { return pow(a, b); }
+
+// integer operands of a float-only function are promoted to fp32 first
+__device__ __forceinline__ float exp_(int64_t x) { return expf(static_cast<float>(x)); }
+__device__ __forceinline__ float log_(int64_t x) { return logf(static_cast<float>(x)); }
+__device__ __forceinline__ float sqrt_(int64_t x) { return sqrtf(static_cast<float>(x)); }
+__device__ __forceinline__ float rsqrt_(int64_t x) { return 1.0f / sqrtf(static_cast<float>(x)); }
+__device__ __forceinline__ float tanh_(int64_t x) { return tanhf(static_cast<float>(x)); }
+__device__ __forceinline__ float erf_(int64_t x) { return erff(static_cast<float>(x)); }
+__device__ __forceinline__ float sigmoid_(int64_t x) { return sigmoid_(static_cast<float>(x)); }
+
+template <class T> __device__ __forceinline__ T max_(T a, T b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return a > b ? a : b;
+}
+template <class T> __device__ __forceinline__ T min_(T a, T b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return a < b ? a : b;
+}
+
+// ---------------------------------------------------------------------------
+// reduction operators
+// ---------------------------------------------------------------------------
+struct OpSum {
+  template <class T> __device__ __forceinline__ static T f(T a, T b) { return a + b; }
+};
+struct OpProd {
+  template <class T> __device__ __forceinline__ static T f(T a, T b) { return a * b; }
+};
+struct OpMax {
+  template <class T> __device__ __forceinline__ static T f(T a, T b) { return max_(a, b); }
+};
+struct OpMin {
+  template <class T> __device__ __forceinline__ static T f(T a, T b) { return min_(a, b); }
+};
+
+// ---------------------------------------------------------------------------
+// cross-lane movement (32-bit payloads through DPP / swizzle / readlane;
+// 64-bit payloads through ds_bpermute shuffles)
+// ---------------------------------------------------------------------------
+template <int CTRL> __device__ __forceinline__ float dpp(float x) {
+  const int v = __builtin_bit_cast(int, x);
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false));
+}
+template <int CTRL> __device__ __forceinline__ int dpp(int x) {
+  return __builtin_amdgcn_update_dpp(x, x, CTRL, 0xf, 0xf, false);
+}
+template <int PATTERN> __device__ __forceinline__ float swizzle(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), PATTERN));
+}
+template <int PATTERN> __device__ __forceinline__ int swizzle(int x) {
+  return __builtin_amdgcn_ds_swizzle(x, PATTERN);
+}
+__device__ __forceinline__ float readlane(float x, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+constexpr int kQuadSwap1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kQuadSwap2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+constexpr int kSwizzleXor16 = 0x401F; // bit-mask mode: and 0x1f, or 0, xor 0x10
+
+// Reduce over aligned groups of G lanes (G a power of two <= 64); every lane
+// of a group ends with the same value.
+template <int G, class Op>
+__device__ __forceinline__ float group_reduce(float x) {
+  if constexpr (G >= 2) x = Op::f(x, dpp<kQuadSwap1>(x));
+  if constexpr (G >= 4) x = Op::f(x, dpp<kQuadSwap2>(x));
+  if constexpr (G >= 8) x = Op::f(x, dpp<kRowHalfMirror>(x));
+  if constexpr (G >= 16) x = Op::f(x, dpp<kRowMirror>(x));
+  if constexpr (G >= 32) x = Op::f(x, swizzle<kSwizzleXor16>(x));
+  if constexpr (G >= 64) x = Op::f(readlane(x, 0), readlane(x, 32));
+  return x;
+}
+
+template <int G, class Op, class T>
+__device__ __forceinline__ T group_reduce(T x) {
+#pragma unroll
+  for (int m = 1; m < G; m <<= 1) x = Op::f(x, __shfl_xor(x, m, 64));
+  return x;
+}
+
+// Reduce over a row spread across W = G/64 whole waves of one workgroup.
+// ``slot`` is this reduction's private LDS array of W entries.
+template <int G, class Op, class T>
+__device__ __forceinline__ T block_reduce(T x, T* slot) {
+  static_assert(G % 64 == 0, "block_reduce spans whole waves");
+  constexpr int W = G / 64;
+  x = group_reduce<64, Op>(x);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) slot[wave] = x;
+  __syncthreads();
+  T r = slot[0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) r = Op::f(r, slot[w]);
+  return r;
+}
+
+template <int G, class Op, class T>
+__device__ __forceinline__ T row_reduce(T x, T* slot) {
+  if constexpr (G <= 64) {
+    (void)slot;
+    return group_reduce<G, Op>(x);
+  } else {
+    return block_reduce<G, Op>(x, slot);
+  }
+}
+
+}  // namespace mlc

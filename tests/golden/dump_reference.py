@@ -1,0 +1,132 @@
+"""Write golden fixtures from the reference compiler (run in the build
+container only; the GPU box never has the reference).
+
+What the fixtures pin, per case: the schedule (kernel kinds, order, operand
+buffers and rendered index strings, reduce kinds, row outputs), the arena
+size, lower bound, unplanned total and every arena offset, plus -- for the
+toy models -- the reference's torch-backend outputs. Nothing else pins these:
+the published numbers only give kernel counts and arena totals.
+
+Usage (from the repository root)::
+
+    python tests/golden/dump_reference.py /root/reference tests/golden/reference_schedules.json
+
+The reference is imported from the path given; the script runs in its own
+process so the reference's ``mlc`` package never meets this repository's.
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+
+
+def _describe(sched):
+    from mlc.kernels import ExternKernel, PointwiseKernel, ReductionKernel
+
+    out = []
+    for k in sched.kernels:
+        d = {"name": k.name, "summary": k.summary()}
+        if isinstance(k, ExternKernel):
+            d["kind"] = "extern"
+            d["op"] = k.node.op
+            d["inputs"] = [v.buffer.name for v in k.inputs]
+            d["outputs"] = [v.buffer.name for v in k.outputs]
+        else:
+            d["kind"] = "pointwise" if isinstance(k, PointwiseKernel) else "reduction"
+            d["inputs"] = [[a.value.buffer.name, str(a.dtype), a.index.render()] for a in k.inputs]
+            d["outputs"] = [[a.value.buffer.name, str(a.dtype), a.index.render()] for a in k.outputs]
+            d["ops"] = [n.op for n in k.nodes]
+            if isinstance(k, PointwiseKernel):
+                d["space"] = list(k.space)
+                d["body"] = [[t, repr(e)] for t, e in k.body]
+            else:
+                d["row_space"] = list(k.row_space)
+                d["reduce_space"] = list(k.reduce_space)
+                d["reduces"] = [r.kind for r in k.reduces]
+                d["steps"] = [[s.name, type(s).__name__, repr(s.expr)] for s in k.steps]
+                d["row_outputs"] = sorted(k.row_outputs)
+                d["two_pass"] = bool(k.two_pass)
+            d["out_expr"] = {n: repr(e) for n, e in sorted(k.out_expr.items())}
+        out.append(d)
+    return out
+
+
+def _plan(sched):
+    p = sched.plan
+    return {"mode": p.mode, "arena_bytes": p.arena_bytes, "peak_bytes": p.peak_bytes,
+            "total_bytes": p.total_bytes, "offsets": dict(sorted(p.offsets.items()))}
+
+
+def main(ref_root: str, out_path: str) -> None:
+    sys.path.insert(0, ref_root)
+    sys.path.insert(0, ref_root + "/tests")
+    import torch
+
+    import mlc
+    from mlc.api import build_pipeline
+    from mlc.bench.models import build
+    from mlc.config import Config
+    from mlc.ir.capture import capture
+    from models import all_models
+
+    configs = {
+        "no_fusion": Config(elementwise_fusion=False, recompute=False, reduction_fusion=False,
+                            memory_planning=False, cuda_graphs=False),
+        "elementwise": Config(reduction_fusion=False, recompute=False, memory_planning=False,
+                              cuda_graphs=False),
+        "planned": Config(reduction_fusion=False, cuda_graphs=False),
+        "all_passes": Config(cuda_graphs=False),
+        "streamed": Config(cuda_graphs=False, max_persistent_row=4),
+        "graphs": Config(),
+    }
+    result = {"torch": torch.__version__, "toy": {}, "bench": {}}
+
+    for name, model, args in all_models():
+        entry = {}
+        for cname, cfg in configs.items():
+            g = capture(model, args)
+            sched = build_pipeline(g, cfg)
+            rec = {"kernels": _describe(sched), "plan": _plan(sched),
+                   "counts": sched.counts(), "graph_nodes": len(g.nodes)}
+            if cname in ("all_passes", "streamed", "no_fusion"):
+                torch.manual_seed(0)
+                got = mlc.compile(model, args, cfg)(*args)
+                outs = got if isinstance(got, (list, tuple)) else [got]
+                rec["outputs"] = [o.detach().double().reshape(-1).tolist() for o in outs]
+                rec["output_shapes"] = [list(o.shape) for o in outs]
+            entry[cname] = rec
+        result["toy"][name] = entry
+
+    bench_cases = [
+        ("bert-base", 1, 128, torch.float16),
+        ("bert-base", 32, 128, torch.float16),
+        ("bert-base", 1, 128, torch.float32),
+        ("gpt2-small", 1, 128, torch.float16),
+        ("gpt2-small", 32, 128, torch.float16),
+        ("gpt2-small", 32, 512, torch.float16),
+        ("gpt-small", 1, 32, torch.float32),
+        ("gpt-small", 2, 32, torch.float32),
+        ("bert-small", 1, 32, torch.float32),
+        ("bert-small", 2, 32, torch.float32),
+    ]
+    for mname, batch, seq, dt in bench_cases:
+        model, args = build(mname, batch, seq, "cpu", dt)
+        g = capture(model, args)
+        for cname in ("graphs", "streamed64"):
+            cfg = Config() if cname == "graphs" else Config(max_persistent_row=64)
+            if cname == "streamed64" and not (mname == "bert-base" and batch == 1 and dt == torch.float16):
+                continue
+            g = capture(model, args)
+            sched = build_pipeline(g, cfg)
+            key = f"{mname}|b{batch}|s{seq}|{str(dt).replace('torch.', '')}|{cname}"
+            result["bench"][key] = {"kernels": _describe(sched), "plan": _plan(sched),
+                                    "counts": sched.counts(), "graph_nodes": len(g.nodes)}
+            print(key, sched.counts(), sched.plan.arena_bytes, flush=True)
+
+    with open(out_path, "w") as f:
+        json.dump(result, f, indent=0, sort_keys=True)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1], sys.argv[2])
