@@ -1,0 +1,54 @@
+"""Algorithmic HBM bytes of a generated kernel, the unit the bandwidth
+roofline is priced in.
+
+    bytes(k) = sum over distinct (buffer, index map) inputs of
+                   (distinct elements addressed) * itemsize
+             + sum over outputs of (elements written) * itemsize
+
+An index map's distinct elements are the product of the sizes of its
+canonical terms (stride-0 dims are already dropped, so a broadcast operand
+counts once). This equals the reference cost model's traffic
+(``mlc/passes/cost.py:44-59``) when no operand is broadcast-expanded.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ..codegen.index import IndexMap
+from ..kernels import ExternKernel, PointwiseKernel, ReductionKernel
+
+#: MI355X published peak HBM3E bandwidth, GB/s
+HBM_PEAK_GBS = 8000.0
+
+
+def _itemsize(dtype: torch.dtype) -> int:
+    return torch.empty((), dtype=dtype).element_size()
+
+
+def distinct_elements(imap: IndexMap) -> int:
+    return math.prod(size for a in imap.axes for size, _, _ in a.terms)
+
+
+def algorithmic_bytes(k) -> int:
+    if isinstance(k, ExternKernel):
+        if k.node.op == "aten.embedding.default":
+            out = k.outputs[0]
+            ids = k.node.args[1]
+            return 2 * out.numel * _itemsize(out.dtype) + ids.numel * _itemsize(ids.dtype)
+        raise TypeError(f"no byte model for extern {k.node.op}")
+    if not isinstance(k, (PointwiseKernel, ReductionKernel)):
+        raise TypeError(type(k).__name__)
+    seen = set()
+    total = 0
+    for a in k.inputs:
+        key = (a.value.buffer.name, a.index.render())
+        if key in seen:
+            continue
+        seen.add(key)
+        total += distinct_elements(a.index) * _itemsize(a.dtype)
+    for a in k.outputs:
+        total += distinct_elements(a.index) * _itemsize(a.dtype)
+    return total

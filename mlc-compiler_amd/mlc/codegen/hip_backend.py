@@ -42,7 +42,8 @@ import torch
 from ..config import Config
 from ..ir.scalar import Call, Cast, Const, Expr, Load, Ref, loads as expr_loads, refs as expr_refs
 from ..kernels import Bind, ExternKernel, PointwiseKernel, Reduce, ReductionKernel, Schedule
-from .index import IndexMap
+from ..ir.graph import Value
+from .index import IndexMap, build_index
 from .reduction_schedule import plan_passes, scalar_binds, varies_by_column
 
 WAVE = 64
@@ -672,7 +673,7 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
         e = k.out_expr[nm]
         acc = _row_col_access(k, a, V)
         ot = compute_type_of_out(k, a)
-        L.append(f"  {{ // store {nm}")
+        L.append(f"  {{ // store out{i}")
         L.append(f"    const {it} rb = {offs.row(a)};")
         L.append("#pragma unroll")
         L.append("    for (int p = 0; p < K; ++p) {")
@@ -902,6 +903,107 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
 
 
 # --------------------------------------------------------------------------
+# extern ops with a native template
+# --------------------------------------------------------------------------
+
+EMBED_BLOCK = 256
+
+
+def emit_extern(k: ExternKernel, cfg: Config | None = None) -> tuple[str, LaunchSpec] | None:
+    if k.node.op == "aten.embedding.default":
+        return emit_embedding(k)
+    return None
+
+
+def emit_embedding(k: ExternKernel) -> tuple[str, LaunchSpec] | None:
+    """``out[i, :] = weight[ids[i], :]`` -- the forward of ``aten.embedding``
+    as a bit copy of 128-bit packs, one thread per pack. An id outside
+    ``[0, rows of weight)`` yields a zero row and sets the error word (torch
+    raises for such an id; the host reads the word back)."""
+    node = k.node
+    if len(node.args) < 2 or len(node.outputs) != 1:
+        return None
+    weight, ids = node.args[0], node.args[1]
+    out = node.outputs[0]
+    if not isinstance(weight, Value) or not isinstance(ids, Value) or len(weight.shape) != 2:
+        return None
+    if ids.dtype not in (torch.int64, torch.int32) or weight.dtype not in STORAGE:
+        return None
+    NV, D = weight.shape
+    rows = math.prod(ids.shape) if ids.shape else 1
+    if out.dtype != weight.dtype or tuple(out.shape) != tuple(ids.shape) + (D,):
+        return None
+    id_map = build_index([("row", ids.shape)], ids.layout)
+    w_map = build_index([("vrow", (NV,)), ("col", (D,))], weight.layout)
+    o_map = build_index([("row", ids.shape), ("col", (D,))], out.layout)
+    big = max(weight.buffer.numel, out.buffer.numel, ids.buffer.numel) >= 2 ** 31
+    it = "uint64_t" if big else "uint32_t"
+    V = max(1, 16 // itemsize(weight.dtype))
+
+    def unit_col(imap):
+        return axis_terms(imap, "col") in (((D, 1, 1),), ()) if D > 1 else True
+
+    def aligned(imap, var_row):
+        others = [t[2] for t in axis_terms(imap, var_row)] + [imap.base]
+        return all(o % V == 0 for o in others)
+
+    while V > 1 and not (D % V == 0 and unit_col(w_map) and unit_col(o_map)
+                         and aligned(w_map, "vrow") and aligned(o_map, "row")):
+        V //= 2
+    P = D // V if D % V == 0 else D
+    if P * V != D:
+        V, P = 1, D
+    vrow_terms = axis_terms(w_map, "vrow")
+    w_stride = vrow_terms[0][2] if vrow_terms else 0
+    w_col = axis_terms(w_map, "col")
+    w_cs = w_col[0][2] if w_col else 0
+    o_col = axis_terms(o_map, "col")
+    o_cs = o_col[0][2] if o_col else 0
+
+    def row_off(imap) -> str:
+        parts = render_terms(axis_terms(imap, "row"), rows, "row", it)
+        if imap.base:
+            parts.append(f"({it}){imap.base}")
+        return join_offset(parts, it)
+
+    S = STORAGE[weight.dtype]
+    I = STORAGE[ids.dtype]
+    L = [f"extern \"C\" __global__ void __launch_bounds__({EMBED_BLOCK}) "
+         f"KERNEL(const {S}* __restrict__ in0, const {I}* __restrict__ in1, "
+         f"{S}* __restrict__ out0, int* __restrict__ err) {{",
+         f"  // embedding: {rows} ids into a [{NV}, {D}] table, {V}-element packs",
+         f"  constexpr {it} P = ({it}){P};",
+         f"  constexpr int V = {V};",
+         f"  const {it} g = ({it})blockIdx.x * {EMBED_BLOCK} + threadIdx.x;",
+         f"  if (g >= ({it}){rows} * P) return;",
+         f"  const {it} row = g / P;",
+         f"  const {it} col = (g % P) * V;",
+         f"  const int64_t id = (int64_t)in1[{row_off(id_map)}];",
+         f"  {S}* dst = out0 + {row_off(o_map)} + col * ({it}){o_cs};",
+         f"  if (id < 0 || id >= (int64_t){NV}) {{",
+         f"#pragma unroll",
+         f"    for (int j = 0; j < V; ++j) dst[({it})j * ({it}){o_cs}] = mlc::cvt<{S}>(0.0f);",
+         f"    *err = 1;",
+         f"    return;",
+         f"  }}",
+         f"  const {S}* src = in0 + ({it}){w_map.base} + ({it})id * ({it}){w_stride} + col * ({it}){w_cs};"]
+    if V > 1:
+        L.append(f"  *reinterpret_cast<mlc::pack<{S}, V>*>(dst) = "
+                 f"*reinterpret_cast<const mlc::pack<{S}, V>*>(src);")
+    else:
+        L.append("  *dst = *src;")
+    L.append("}")
+    total = rows * P
+    spec = LaunchSpec("", max(1, -(-total // EMBED_BLOCK)), EMBED_BLOCK, 0,
+                      {"kind": "embedding", "vec": V, "rows": rows, "cols": D, "table_rows": NV,
+                       "buffers": [weight.buffer.name, ids.buffer.name, out.buffer.name],
+                       "dtypes": [weight.dtype, ids.dtype, out.dtype],
+                       "numels": [weight.buffer.numel, ids.buffer.numel, out.buffer.numel],
+                       "error_word": True})
+    return "\n".join(L), spec
+
+
+# --------------------------------------------------------------------------
 # module
 # --------------------------------------------------------------------------
 
@@ -919,22 +1021,28 @@ class Module:
     functions: dict[str, str]
 
 
-def emit_kernel(k, cfg: Config) -> tuple[str, LaunchSpec]:
+def emit_kernel(k, cfg: Config) -> tuple[str, LaunchSpec] | None:
+    """Source and launch spec of one kernel; ``None`` for an extern op that
+    stays a library call."""
     if isinstance(k, PointwiseKernel):
         return emit_pointwise(k, cfg)
     if isinstance(k, ReductionKernel):
         return emit_reduction(k, cfg)
+    if isinstance(k, ExternKernel):
+        return emit_extern(k, cfg)
     raise TypeError(f"no HIP emitter for {type(k).__name__}")
 
 
 def generate_module(schedule: Schedule, cfg: Config) -> Module:
-    """Every generated kernel of ``schedule`` as one HIP translation unit."""
+    """Every generated kernel of ``schedule`` (and every extern op with a
+    native template) as one HIP translation unit."""
     functions: dict[str, str] = {}
     launches: dict[str, LaunchSpec] = {}
     for k in schedule.kernels:
-        if isinstance(k, ExternKernel):
+        emitted = emit_kernel(k, cfg)
+        if emitted is None:
             continue
-        body, spec = emit_kernel(k, cfg)
+        body, spec = emitted
         digest = hashlib.sha256(body.encode()).hexdigest()[:16]
         symbol = f"mlc_{digest}"
         functions.setdefault(symbol, body.replace("KERNEL(", f"{symbol}(", 1))

@@ -255,12 +255,29 @@ class CompiledModel:
             after = _alloc_count(self.device)
         torch.cuda.current_stream(self.device).wait_stream(side)
         if after != before:
+            culprits = self._allocating_entries(side)
             raise ExecutionError(f"{after - before} device allocation(s) happened during graph "
-                                 "capture; the captured graph would reference memory it does not own")
+                                 "capture; the captured graph would reference memory it does not "
+                                 f"own (allocating entries: {culprits})")
         self._capture_stream = side
         self._captured = True
         self._static_inputs = [buffers[v.buffer.name] for v in self.graph.inputs]
         self._static_outputs = self._collect(buffers)
+
+    def _allocating_entries(self, stream) -> list[str]:
+        """Plan entries that allocate device memory each time they run."""
+        found = []
+        with torch.cuda.stream(stream):
+            for kernel, (kind, payload) in zip(self.schedule.kernels, self._plan):
+                before = _alloc_count(self.device)
+                if kind == "extern":
+                    run_bound_extern(payload)
+                else:
+                    self._module.run_bound(payload)
+                if _alloc_count(self.device) != before:
+                    found.append(kernel.summary())
+        stream.synchronize()
+        return found
 
     def profile_kernels(self, inputs, iters: int = 20) -> list[tuple]:
         """(name, summary, ms) per kernel, each timed in place on the launch

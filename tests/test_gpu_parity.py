@@ -1,0 +1,177 @@
+"""GPU parity: the HIP backend against the CPU oracle on identical seeded
+inputs.
+
+* every toy model under every pass configuration, end to end, at the
+  reference's fp32 bar (``tests/test_correctness.py:17`` of the reference:
+  rtol 1e-5, atol 1e-6);
+* BASELINE config 1 (FFN block, fp32): max error relative to the output's
+  largest magnitude <= 1e-5;
+* BERT-base and GPT-2 small fp16 (configs 2 and 3): every generated kernel
+  checked on identical inputs (lockstep) at max relative error <= 2e-3 (fp16
+  outputs) / 1e-5 (fp32 outputs), native extern templates bit-exact; the
+  final outputs of the free-running HIP model within 2e-3 of the float64
+  result and no further from the oracle chain than eager PyTorch is.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import mlc
+from gpu_util import flat_outputs, lockstep, rel_err
+from mlc.api import build_pipeline
+from mlc.bench.workloads import make
+from mlc.config import Config
+from mlc.ir.capture import capture
+from mlc.runtime.hip_runtime import HipRuntime
+from models import all_models
+from oracle import compile_reference
+
+pytestmark = pytest.mark.gpu
+
+CONFIGS = {
+    "no_fusion": Config(elementwise_fusion=False, recompute=False, reduction_fusion=False,
+                        memory_planning=False, cuda_graphs=False),
+    "elementwise": Config(reduction_fusion=False, recompute=False, memory_planning=False,
+                          cuda_graphs=False),
+    "planned": Config(reduction_fusion=False, cuda_graphs=False),
+    "all_passes": Config(cuda_graphs=False),
+    "streamed": Config(cuda_graphs=False, max_persistent_row=4),
+    "graphs": Config(),
+}
+
+
+def _to(args, device):
+    return tuple(a.to(device) for a in args)
+
+
+@pytest.mark.parametrize("cname", list(CONFIGS))
+@pytest.mark.parametrize("name", [m[0] for m in all_models()])
+def test_toy_models(name, cname):
+    cfg = CONFIGS[cname]
+    _, model, args = next(t for t in all_models() if t[0] == name)
+    want = compile_reference(model, args, cfg)(*args)
+    compiled = mlc.compile(model.to("cuda"), _to(args, "cuda"), cfg)
+    got = compiled(*_to(args, "cuda"))
+    torch.cuda.synchronize()
+    for g, w in zip(flat_outputs(got), flat_outputs(want)):
+        torch.testing.assert_close(g.cpu(), w, rtol=1e-5, atol=1e-6)
+    model.to("cpu")
+
+
+def test_config1_ffn_block():
+    model, args = make("C1", "cpu")
+    want = compile_reference(model, args)(*args)
+    gm, ga = make("C1", "cuda")
+    got = mlc.compile(gm, ga)(*ga)
+    torch.cuda.synchronize()
+    assert rel_err(got, want) <= 1e-5
+
+
+def _params_by_buffer(graph):
+    return {v.buffer.name: graph.param_tensors[v.name].detach().cpu().contiguous().reshape(-1)
+            for v in graph.params}
+
+
+@pytest.mark.parametrize("key", ["C2", "C3"])
+def test_lockstep_every_kernel(key):
+    """Each generated kernel of the fp16 model, fed the oracle's own inputs:
+    fp16 outputs within 2 ulp-scale (2e-3 relative to the largest magnitude),
+    fp32/int outputs tighter."""
+    model, args = make(key, "cpu")
+    cfg = Config()
+    graph = capture(model, args)
+    schedule = build_pipeline(graph, cfg)
+    rt = HipRuntime(schedule, cfg, torch.device("cuda:0"))
+    worst = {}
+
+    def check(k, name, got, want):
+        if want.is_floating_point():
+            err = rel_err(got, want)
+            tol = 2e-3 if want.dtype in (torch.float16, torch.bfloat16) else 1e-5
+            worst[k.name] = err
+            assert err <= tol, f"{k.summary()}: output {name} rel err {err:.3e} > {tol}"
+        else:
+            assert torch.equal(got, want), f"{k.summary()}: output {name} differs"
+
+    lockstep(schedule, graph, _params_by_buffer(graph), args, rt, check)
+    assert len(worst) > 0
+    print(key, "worst per-kernel rel err", max(worst.values()))
+
+
+def _truth_fp64(key):
+    model, args = make(key, "cpu")
+    model = model.double()
+    args = tuple(a.double() if a.is_floating_point() else a for a in args)
+    with torch.no_grad():
+        return flat_outputs(model(*args))
+
+
+@pytest.mark.parametrize("key", ["C2", "C3"])
+def test_end_to_end_fp16(key):
+    """Free-running HIP model (hipGraph replay) end to end in fp16.
+
+    Two fp16 implementations of a 12-layer model drift apart: wherever their
+    fp32 results differ in the last bit, an fp16 rounding can flip, and the
+    flips propagate through every later layer. Eager PyTorch on the GPU and
+    the oracle chain already differ by ~3e-3 on BERT's pooled output. So the
+    2e-3 bar is applied against the exact result (the model in float64 on the
+    CPU), and the distance to the oracle chain (CPU oracle kernels sharing the
+    GPU's extern results) must be no larger than eager PyTorch's.
+    """
+    model, args = make(key, "cpu")
+    cfg = Config()
+    graph = capture(model, args)
+    schedule = build_pipeline(graph, cfg)
+    rt = HipRuntime(schedule, cfg, torch.device("cuda:0"))
+    ref = lockstep(schedule, graph, _params_by_buffer(graph), args, rt, None)
+    gm, ga = make(key, "cuda")
+    compiled = mlc.compile(gm, ga, cfg)
+    got = flat_outputs(compiled(*ga))
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        eager = flat_outputs(gm(*ga))
+    truth = _truth_fp64(key)
+    for g, v, e, t in zip(got, graph.outputs, eager, truth):
+        want = v.layout.as_torch(ref[v.buffer.name])
+        hip_truth, hip_oracle = rel_err(g, t), rel_err(g, want)
+        oracle_truth, eager_oracle, eager_truth = rel_err(want, t), rel_err(e, want), rel_err(e, t)
+        print(f"{key} {v.name} {tuple(g.shape)}: hip-vs-fp64 {hip_truth:.2e}, "
+              f"oracle-vs-fp64 {oracle_truth:.2e}, eager-vs-fp64 {eager_truth:.2e}, "
+              f"hip-vs-oracle {hip_oracle:.2e}, eager-vs-oracle {eager_oracle:.2e}")
+        assert hip_truth <= 2e-3
+        assert hip_oracle <= max(2e-3, eager_oracle)
+        # and against eager PyTorch at the reference's fp16 bar
+        # (tests/test_dtypes.py:35-58 of the reference: rtol 1e-2, atol 5e-2)
+        torch.testing.assert_close(g.float(), e.float(), rtol=1e-2, atol=5e-2)
+
+
+def test_graph_replay_matches_plan_run():
+    """The captured hipGraph and the un-captured plan produce bit-identical
+    outputs, replay after replay, and the graph holds every kernel."""
+    gm, ga = make("C2", "cuda")
+    eager_cfg = Config(cuda_graphs=False)
+    plain = mlc.compile(gm, ga, eager_cfg)
+    want = plain(*ga).clone()
+    compiled = mlc.compile(gm, ga, Config())
+    for _ in range(3):
+        got = compiled(*ga)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+    assert compiled._module.graph_nodes() >= len(compiled.schedule.kernels)
+
+
+def test_arena_is_one_slab_with_planned_offsets():
+    gm, ga = make("C2", "cuda")
+    compiled = mlc.compile(gm, ga, Config())
+    compiled(*ga)
+    torch.cuda.synchronize()
+    arena = compiled._arena
+    plan = compiled.schedule.plan
+    assert arena.numel() >= plan.arena_bytes == 1769728
+    base = arena.data_ptr()
+    for name, off in plan.offsets.items():
+        t = compiled._resident.get(name)
+        if t is not None:
+            assert t.data_ptr() == base + off
