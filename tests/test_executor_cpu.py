@@ -1,0 +1,96 @@
+"""Executor behaviour on the CPU, with the oracle as the kernel runner (the
+product's buffer table, arena binding, extern dispatch and output aliasing are
+the code under test), plus the rule that the product itself never runs
+anywhere but the GPU (``mlc/runtime/executor.py`` of the reference,
+``tests/test_correctness.py:101-171``)."""
+
+from __future__ import annotations
+
+import subprocess
+import sys
+
+import pytest
+import torch
+
+import mlc
+from mlc.config import Config
+from mlc.runtime.executor import ExecutionError, select_backend
+from models import all_models
+from oracle import compile_reference
+
+FULL = Config(cuda_graphs=False)
+
+
+def _model(name):
+    return next(t for t in all_models() if t[0] == name)
+
+
+def test_wrong_input_shape_is_rejected():
+    _, model, args = _model("pointwise")
+    compiled = compile_reference(model, args, FULL)
+    with pytest.raises(ExecutionError, match="compiled for"):
+        compiled(torch.randn(5, 16), torch.randn(5, 16))
+
+
+def test_outputs_alias_static_storage():
+    _, model, args = _model("residual_chain")
+    compiled = compile_reference(model, args, FULL)
+    first = compiled(*args)
+    kept = first.clone()
+    second = compiled(args[0] * 2)
+    assert second.data_ptr() == first.data_ptr()
+    assert not torch.equal(first, kept), "the first result is overwritten by the next call"
+
+
+def test_inputs_are_copied_not_aliased():
+    _, model, args = _model("pointwise")
+    compiled = compile_reference(model, args, FULL)
+    x = args[0].clone()
+    out = compiled(x, args[1]).clone()
+    x.add_(100.0)
+    again = compiled(args[0], args[1])
+    torch.testing.assert_close(again, out, rtol=0, atol=0)
+
+
+def test_arena_offsets_bind_buffers():
+    _, model, args = _model("block")
+    compiled = compile_reference(model, args, FULL)
+    compiled(*args)
+    arena = compiled._arena
+    plan = compiled.schedule.plan
+    assert arena.numel() == plan.arena_bytes
+    for name, off in plan.offsets.items():
+        t = compiled._resident.get(name)
+        if t is not None:
+            assert t.untyped_storage().data_ptr() == arena.untyped_storage().data_ptr()
+            assert t.data_ptr() - arena.data_ptr() == off
+
+
+def test_product_refuses_the_cpu():
+    """No silent CPU fallback: mlc.compile on a CPU model raises."""
+    _, model, args = _model("pointwise")
+    with pytest.raises(ExecutionError, match="ROCm GPU"):
+        mlc.compile(model, args, FULL)
+    with pytest.raises(ExecutionError):
+        select_backend(Config(backend="triton"), torch.device("cuda"))
+    assert select_backend(Config(), torch.device("cuda")) == "hip"
+
+
+def test_hip_runtime_refuses_a_cpu_device():
+    from mlc.runtime.hip_runtime import HipRuntime
+    from mlc.runtime.native import NativeError
+
+    _, model, args = _model("pointwise")
+    from mlc.api import build_pipeline
+    from mlc.ir.capture import capture
+
+    sched = build_pipeline(capture(model, args), FULL)
+    with pytest.raises(NativeError, match="GPU"):
+        HipRuntime(sched, FULL, torch.device("cpu"))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    proc = subprocess.run([sys.executable, "bench.py", "--gpus", "2"], capture_output=True,
+                          text=True, cwd=str(__import__("pathlib").Path(__file__).parents[1]))
+    assert proc.returncode == 2
+    assert "one GPU" in proc.stderr
