@@ -7,8 +7,9 @@ One step is one forward of the compiled model (one hipGraph replay: every
 generated kernel plus every extern library call) over inputs already resident
 in HBM. ``value`` is ms per forward at b1; b32 (config 4)
 is timed the same way and reported beside it. The roofline object covers the
-dominant fused kernel at b32 (the one with the most device time), timed with
-hipEvents on its launch stream; ``fused_b32`` aggregates every fused kernel.
+dominant fused kernel at b32 (the function moving the most algorithmic bytes
+per forward), timed with hipEvents on its launch stream, with its
+counter-measured traffic from the committed PMC summary in ``profiles/``; ``fused_b32`` aggregates every fused kernel.
 The CPU baseline is the oracle (the kernel IR executed with torch on the
 host) on a bounded number of b1 forwards. Prints one JSON line.
 """
@@ -79,6 +80,18 @@ def _kernel_table(compiled, iters: int):
     return rows
 
 
+def _measured_traffic(symbol: str):
+    """Counter-measured HBM bytes per launch of ``symbol`` from the committed
+    PMC summary (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a
+    plain copy of known size), or None when that summary is for other code."""
+    for path in sorted((ROOT / "profiles").glob("*.md")):
+        for line in path.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == symbol:
+                return int(parts[2])
+    return None
+
+
 def _cpu_baseline(key: str, budget_s: float):
     import torch
 
@@ -145,14 +158,16 @@ def main() -> int:
         del compiled, model, inputs
         torch.cuda.empty_cache()
 
-    # dominant fused kernel at b32: the symbol with the most device time per forward
+    # dominant fused kernel at b32: the function moving the most algorithmic
+    # bytes per forward (a property of the schedule, not of one timing run)
     rows = tables["C4"]
     per_symbol = {}
     for k, sym, nbytes, ms in rows:
-        agg = per_symbol.setdefault(sym, {"ms": 0.0, "bytes": nbytes, "launch_ms": [], "kernel": k})
-        agg["ms"] += ms
+        agg = per_symbol.setdefault(sym, {"total_bytes": 0, "bytes": nbytes, "launch_ms": [],
+                                          "kernel": k})
+        agg["total_bytes"] += nbytes
         agg["launch_ms"].append(ms)
-    dom_sym = max(per_symbol, key=lambda s: per_symbol[s]["ms"])
+    dom_sym = max(per_symbol, key=lambda s: per_symbol[s]["total_bytes"])
     dom = per_symbol[dom_sym]
     launch_ms = statistics.mean(dom["launch_ms"])
     achieved = dom["bytes"] / (launch_ms * 1e-3) / 1e9
@@ -191,7 +206,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": _measured_traffic(dom_sym),
         },
         "fused_b32": {
             "kernels": len(rows),
