@@ -37,6 +37,7 @@ import math
 import struct
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from ..config import Config
@@ -47,7 +48,6 @@ from .index import IndexMap, build_index
 from .reduction_schedule import plan_passes, scalar_binds, varies_by_column
 
 WAVE = 64
-POINTWISE_BLOCK = 256
 
 #: storage type of each buffer dtype in device code
 STORAGE = {
@@ -156,6 +156,13 @@ class Renderer:
         if fn == "div":
             if _RANK[top] <= _RANK["int64_t"]:
                 return f"((float)({a}) / (float)({codes[1]}))", "float"
+            if top == "float":
+                fast = _const_divisor(e.args[1])
+                if fast is not None:
+                    c, y, exact_mul = fast
+                    if exact_mul:
+                        return f"({a} * {float_literal(y)})", "float"
+                    return f"mlc::div_rcp({a}, {float_literal(c)}, {float_literal(y)})", "float"
             return f"({a} / {codes[1]})", top
         if fn in ("gt", "lt", "ge", "le", "eq", "ne"):
             op = {"gt": ">", "lt": "<", "ge": ">=", "le": "<=", "eq": "==", "ne": "!="}[fn]
@@ -190,6 +197,40 @@ class Renderer:
             arg = a if types[0] in ("float", "double", "int64_t") else f"(float)({a})"
             return f"mlc::{fn}_({arg})", t
         raise KeyError(f"no HIP form for scalar function {fn!r}")
+
+
+def _fp32(v: float) -> float:
+    return float(np.float32(v))
+
+
+def _const_divisor(d: Expr):
+    """(c, RN(1/c), whether x*RN(1/c) is exact) for a constant fp32 divisor
+    in the normal range, else None. A power-of-two divisor has an exact
+    reciprocal, so the division is a multiplication; any other one goes
+    through ``mlc::div_rcp`` (Markstein), which returns the correctly rounded
+    quotient."""
+    if not isinstance(d, Const) or isinstance(d.value, bool) or d.dtype == torch.bool:
+        return None
+    if d.dtype in (torch.float16, torch.bfloat16):
+        c = _round_half(float(d.value), d.dtype)
+    elif d.dtype in (None, torch.float32) or (isinstance(d.value, int) and d.dtype is None):
+        c = _fp32(float(d.value))
+    else:
+        return None
+    if not math.isfinite(c) or c == 0.0 or not (2.0 ** -120 < abs(c) < 2.0 ** 120):
+        return None
+    y = float(np.float32(1.0) / np.float32(c))
+    mant = math.frexp(abs(c))[0]
+    return c, y, mant == 0.5
+
+
+def _scalar_division(expr: Expr, scalars: set[str]):
+    """(numerator, divisor name) when ``expr`` divides by a row-uniform fp32
+    temporary (a reduce result or a row-scalar bind)."""
+    if (isinstance(expr, Call) and expr.fn == "div" and isinstance(expr.args[1], Ref)
+            and expr.args[1].name in scalars):
+        return expr.args[0], expr.args[1].name
+    return None
 
 
 def cast_code(code: str, dtype: torch.dtype) -> tuple[str, str]:
@@ -336,14 +377,20 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
 
     in_types = [compute_type(a.dtype) for a in k.inputs]
     temp_types: dict[str, str] = {}
+    packs = -(-N // V)
+    B, U = pointwise_geometry(packs)
     L: list[str] = []
-    L.append(f"extern \"C\" __global__ void __launch_bounds__({POINTWISE_BLOCK}) "
+    L.append(f"extern \"C\" __global__ void __launch_bounds__({B}) "
              f"KERNEL({', '.join(_params(k))}) {{")
-    L.append(f"  // pointwise over {list(k.space)} = {N} elements, {V}-element packs")
+    L.append(f"  // pointwise over {list(k.space)} = {N} elements, {V}-element packs, "
+             f"{U} per thread")
     L.append(f"  constexpr {it} N = ({it}){N};")
     L.append(f"  constexpr int V = {V};")
-    L.append(f"  const {it} e0 = (({it})blockIdx.x * {POINTWISE_BLOCK} + threadIdx.x) * V;")
-    L.append("  if (e0 >= N) return;")
+    L.append(f"  const {it} base = ({it})blockIdx.x * {B * U} + threadIdx.x;")
+    L.append("#pragma unroll")
+    L.append(f"  for (int u = 0; u < {U}; ++u) {{")
+    L.append(f"  const {it} e0 = (base + ({it})u * {B}) * V;")
+    L.append("  if (e0 >= N) break;")
 
     def body_lines(ref_in, indent: str) -> list[str]:
         lines = []
@@ -414,14 +461,25 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
             L.append(f"      mlc::st(out{i} + {offset(a, 'e')}, {code});")
         L.append("    }")
         L.append("  }")
+    L.append("  }")
     L.append("}")
 
-    packs = -(-N // V)
-    grid = max(1, -(-packs // POINTWISE_BLOCK))
-    spec = LaunchSpec("", grid, POINTWISE_BLOCK, 0,
-                      {"kind": "pointwise", "vec": V, "numel": N,
+    grid = max(1, -(-packs // (B * U)))
+    spec = LaunchSpec("", grid, B, 0,
+                      {"kind": "pointwise", "vec": V, "numel": N, "unroll": U,
                        "access": [a.mode + ("+aligned" if a.aligned else "") for a in accesses]})
     return "\n".join(L), spec
+
+
+#: pointwise launch shape: threads per workgroup, and packs per thread once
+#: a launch has more than ``unroll_above`` packs
+POINTWISE_TUNING = {"block": 512, "unroll": 1, "unroll_above": 1 << 30}
+
+
+def pointwise_geometry(packs: int) -> tuple[int, int]:
+    t = POINTWISE_TUNING
+    u = t["unroll"] if packs > t["unroll_above"] else 1
+    return t["block"], u
 
 
 def compute_type_of_out(k, a) -> str:
@@ -614,6 +672,11 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
 
     elem_r = Renderer(ref_elem, temp_elem)
     scal_r = Renderer(ref_scalar, temp_scalar)
+    rcp_for = _reciprocal_divisors(k, vector)
+
+    def elem_loop(target: str, code: str) -> list[str]:
+        return ["#pragma unroll", "  for (int p = 0; p < K; ++p)", "#pragma unroll",
+                "    for (int j = 0; j < V; ++j)", f"      {target}[p][j] = {code};"]
 
     for s in k.steps:
         if isinstance(s, Bind):
@@ -621,15 +684,21 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
                 code, t = elem_r(s.expr)
                 temp_types[s.name] = t
                 L.append(f"  {t} {s.name}[K][V];")
-                L.append("#pragma unroll")
-                L.append("  for (int p = 0; p < K; ++p)")
-                L.append("#pragma unroll")
-                L.append("    for (int j = 0; j < V; ++j)")
-                L.append(f"      {s.name}[p][j] = {code};")
+                sd = _scalar_division(s.expr, rcp_for)
+                if sd is not None and t == "float":
+                    num, d = elem_r(sd[0])[0], sd[1]
+                    L.append(f"  if (__all(ok_{d})) {{")
+                    L += elem_loop(s.name, f"mlc::div_rcp({num}, {d}, rcp_{d})")
+                    L.append("  } else {")
+                    L += elem_loop(s.name, code)
+                    L.append("  }")
+                else:
+                    L += elem_loop(s.name, code)
             else:
                 code, t = scal_r(s.expr)
                 temp_types[s.name] = t
                 L.append(f"  const {t} {s.name} = {code};")
+                L += _reciprocal_lines(s.name, rcp_for)
             continue
         # Reduce
         code, t = elem_r(s.expr)
@@ -664,6 +733,7 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
         slot = f"lds_{s.name}" if G > WAVE else "nullptr"
         L.append(f"    {s.name} = mlc::row_reduce<G, {op}>(acc, ({t}*){slot});")
         L.append("  }")
+        L += _reciprocal_lines(s.name, rcp_for)
 
     # element stores
     for i, a in enumerate(k.outputs):
@@ -710,6 +780,27 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
                                           "lanes_per_row": G, "packs": K, "rows_per_wg": RPW,
                                           "rows": R, "cols": C})
     return "\n".join(L), spec
+
+
+def _reciprocal_divisors(k: ReductionKernel, vector: set[str]) -> set[str]:
+    """Row-uniform fp32 temporaries that some per-element bind divides by:
+    each gets ``rcp_<name>`` = RN(1/name) once per row."""
+    types = _step_types(k)
+    scalars = {s.name for s in k.steps if isinstance(s, Reduce) or s.name not in vector}
+    found = set()
+    for s in k.steps:
+        if isinstance(s, Bind) and s.name in vector and types[s.name] == "float":
+            sd = _scalar_division(s.expr, scalars)
+            if sd is not None and types.get(sd[1]) == "float":
+                found.add(sd[1])
+    return found
+
+
+def _reciprocal_lines(name: str, rcp_for: set[str], indent: str = "  ") -> list[str]:
+    if name not in rcp_for:
+        return []
+    return [f"{indent}const float rcp_{name} = 1.0f / {name};",
+            f"{indent}const bool ok_{name} = mlc::rcp_ok({name});"]
 
 
 def _step_types(k: ReductionKernel) -> dict[str, str]:
@@ -787,6 +878,7 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
 
     elem_r = Renderer(ref_elem, temp_elem)
     scal_r = Renderer(lambda s: (f"v{s}", in_types[s]), temp_scalar)
+    rcp_for = _reciprocal_divisors(k, vector)
 
     def slots_for(p) -> list[int]:
         used: set[int] = set()
@@ -825,8 +917,19 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
         for b in p.binds:
             code, t = elem_r(b.expr)
             out.append(f"    {t} {b.name}[V];")
-            out.append("#pragma unroll")
-            out.append(f"    for (int j = 0; j < V; ++j) {b.name}[j] = {code};")
+            sd = _scalar_division(b.expr, rcp_for)
+            if sd is not None and t == "float":
+                num, d = elem_r(sd[0])[0], sd[1]
+                out.append(f"    if (__all(ok_{d})) {{")
+                out.append("#pragma unroll")
+                out.append(f"      for (int j = 0; j < V; ++j) {b.name}[j] = mlc::div_rcp({num}, {d}, rcp_{d});")
+                out.append("    } else {")
+                out.append("#pragma unroll")
+                out.append(f"      for (int j = 0; j < V; ++j) {b.name}[j] = {code};")
+                out.append("    }")
+            else:
+                out.append("#pragma unroll")
+                out.append(f"    for (int j = 0; j < V; ++j) {b.name}[j] = {code};")
         if online is not None:
             code, _ = elem_r(online.value)
             out.append("#pragma unroll")
@@ -865,11 +968,13 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             out.append(f"  const float w_{sm} = (m_run == (-__builtin_huge_valf())) ? 0.0f : mlc::exp_(m_run - {mx});")
             slot = f"lds_{sm}" if need_lds else "nullptr"
             out.append(f"  const float {sm} = mlc::row_reduce<G, mlc::OpSum>(l_run * w_{sm}, (float*){slot});")
+            out += _reciprocal_lines(mx, rcp_for) + _reciprocal_lines(sm, rcp_for)
         else:
             for r in p.reduces:
                 t = temp_types[r.name]
                 slot = f"lds_{r.name}" if need_lds else "nullptr"
                 out.append(f"  const {t} {r.name} = mlc::row_reduce<G, {_OP[r.kind]}>(acc_{r.name}, ({t}*){slot});")
+                out += _reciprocal_lines(r.name, rcp_for)
         return out
 
     owner = {r.name: p for p in passes for r in p.reduces}
@@ -885,6 +990,7 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
         elif s.name in scalars:
             code, t = scal_r(s.expr)
             L.append(f"  const {t} {s.name} = {code};")
+            L += _reciprocal_lines(s.name, rcp_for)
     for p in passes:
         if p.stores and not p.reduces:
             L += emit_pass(p)

@@ -154,6 +154,8 @@ __device__ __forceinline__ float tanh_(int64_t x) { return tanhf(static_cast<flo
 __device__ __forceinline__ float erf_(int64_t x) { return erff(static_cast<float>(x)); }
 __device__ __forceinline__ float sigmoid_(int64_t x) { return sigmoid_(static_cast<float>(x)); }
 
+// NaN-propagating max/min (torch.maximum/amax semantics). fp32 maps to the
+// single gfx950 instructions v_maximum3_f32 / v_minimum3_f32.
 template <class T> __device__ __forceinline__ T max_(T a, T b) {
   if (a != a) return a;
   if (b != b) return b;
@@ -163,6 +165,29 @@ template <class T> __device__ __forceinline__ T min_(T a, T b) {
   if (a != a) return a;
   if (b != b) return b;
   return a < b ? a : b;
+}
+template <> __device__ __forceinline__ float max_<float>(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+template <> __device__ __forceinline__ float min_<float>(float a, float b) {
+  return __builtin_elementwise_minimum(a, b);
+}
+
+// x / d given y = RN(1/d): q = RN(x*y), r = x - q*d (exact through the fma),
+// RN(q + r*y) is the correctly rounded quotient (Markstein's theorem, P.
+// Markstein, IBM J. Res. Dev. 34(1), 1990) while d, 1/d and x/d stay in the
+// normal range. An infinite q (x infinite) makes r NaN; q itself is then the
+// quotient. A handful of instructions instead of the IEEE division sequence.
+__device__ __forceinline__ float div_rcp(float x, float d, float y) {
+  const float q = x * y;
+  const float r = __builtin_fmaf(-q, d, x);
+  const float q2 = __builtin_fmaf(r, y, q);
+  return q2 == q2 ? q2 : q;
+}
+// whether div_rcp is exact for every x with this divisor
+__device__ __forceinline__ bool rcp_ok(float d) {
+  const float a = __builtin_fabsf(d);
+  return a > 0x1p-120f && a < 0x1p+120f;
 }
 
 // ---------------------------------------------------------------------------
