@@ -471,6 +471,120 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
     return "\n".join(L), spec
 
 
+TRANSPOSE_TILE = 64
+TRANSPOSE_BLOCK = 256
+
+
+def transpose_pattern(k: PointwiseKernel):
+    """The batched 2-D transpose a pointwise kernel performs, if any.
+
+    Matches one input and one contiguous output where the output's fastest
+    dimension (``r``, size ``Rn``) is strided in the input (``Ri``), the
+    input's unit-stride dimension (``c``, size ``Cn``) sits directly outside it
+    in the output, and every other dimension is a whole ``Rn x Cn`` batch.
+    Returns (Rn, Cn, Ri, batches) or None.
+    """
+    if len(k.inputs) != 1 or len(k.outputs) != 1:
+        return None
+    out, inp = k.outputs[0], k.inputs[0]
+    if not (out.index.base == 0 and axis_terms(out.index, "idx") == ((k.numel, 1, 1),)):
+        return None
+    if inp.dtype != out.dtype or inp.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return None
+    terms = axis_terms(inp.index, "idx")
+    r = [t for t in terms if t[1] == 1]
+    c = [t for t in terms if t[2] == 1]
+    if len(r) != 1 or len(c) != 1 or r[0] is c[0] or r[0][2] == 1:
+        return None
+    Rn, _, Ri = r[0]
+    Cn, Co, _ = c[0]
+    if Co != Rn:
+        return None
+    plane = Rn * Cn
+    if any(t[1] % plane for t in terms if t is not r[0] and t is not c[0]):
+        return None
+    T = TRANSPOSE_TILE
+    if Rn % T or Cn % T:
+        return None
+    V = 16 // itemsize(inp.dtype)
+    others = [t[2] for t in terms if t is not r[0] and t is not c[0]]
+    if inp.index.base % V or Ri % V or any(o % V for o in others):
+        return None
+    return Rn, Cn, Ri, k.numel // plane
+
+
+def emit_transpose(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, LaunchSpec] | None:
+    """A batched transpose copy (with its elementwise body) staged through
+    LDS in 64x64 tiles: 128-bit loads along the input's contiguous dimension,
+    128-bit stores along the output's, so neither side gathers."""
+    pat = transpose_pattern(k)
+    if pat is None:
+        return None
+    Rn, Cn, Ri, nb = pat
+    T, B = TRANSPOSE_TILE, TRANSPOSE_BLOCK
+    inp, out = k.inputs[0], k.outputs[0]
+    S = STORAGE[inp.dtype]
+    V = 16 // itemsize(inp.dtype)
+    it = index_type(k)
+    W = T + 2  # LDS row pitch: the transposed gather hits distinct banks
+    per_thread = (T * T // V) // B
+    in_parts = render_terms(axis_terms(inp.index, "idx"), k.numel, "o0", it)
+    if inp.index.base:
+        in_parts.append(f"({it}){inp.index.base}")
+    in_off = join_offset(in_parts, it)
+    ct = compute_type(inp.dtype)
+    temp_types: dict[str, str] = {}
+    r = Renderer(lambda slot: ("x0", ct), lambda n: (n, temp_types[n]))
+    body = []
+    for name, expr in k.body:
+        code, t = r(expr)
+        temp_types[name] = t
+        body.append(f"      const {t} {name} = {code};")
+    oc, _ = r(k.out_expr[out.value.name])
+    rt_n, ct_n = Rn // T, Cn // T
+    L = [f"extern \"C\" __global__ void __launch_bounds__({B}) "
+         f"KERNEL({', '.join(_params(k))}) {{",
+         f"  // transpose: {nb} x [{Rn} x {Cn}] (row stride {Ri}) -> [{Cn} x {Rn}], "
+         f"{T}x{T} tiles through LDS",
+         f"  constexpr int T = {T}, V = {V}, W = {W};",
+         f"  __shared__ {S} tile[T * W];",
+         f"  const {it} t = blockIdx.x;",
+         f"  const {it} r0 = (t % ({it}){rt_n}) * T;",
+         f"  const {it} c0 = ((t / ({it}){rt_n}) % ({it}){ct_n}) * T;",
+         f"  const {it} b = t / ({it}){rt_n * ct_n};",
+         f"  const {it} o0 = b * ({it}){Rn * Cn} + c0 * ({it}){Rn} + r0;",
+         f"  const {it} i0 = {in_off};",
+         "#pragma unroll",
+         f"  for (int u = 0; u < {per_thread}; ++u) {{",
+         f"    const int id = u * {B} + (int)threadIdx.x;",
+         "    const int rr = id / (T / V), p = id % (T / V);",
+         f"    const mlc::pack<{S}, V> w = *reinterpret_cast<const mlc::pack<{S}, V>*>("
+         f"in0 + i0 + ({it})rr * ({it}){Ri} + ({it})(p * V));",
+         "#pragma unroll",
+         "    for (int j = 0; j < V; ++j) tile[rr * W + p * V + j] = w.x[j];",
+         "  }",
+         "  __syncthreads();",
+         "#pragma unroll",
+         f"  for (int u = 0; u < {per_thread}; ++u) {{",
+         f"    const int id = u * {B} + (int)threadIdx.x;",
+         "    const int cc = id / (T / V), q = id % (T / V);",
+         f"    {compute_type_of_out(k, out)} o[V];",
+         "#pragma unroll",
+         "    for (int j = 0; j < V; ++j) {",
+         "      const auto x0 = mlc::ld(&tile[(q * V + j) * W + cc]);"]
+    L += body
+    L += [f"      o[j] = {oc};",
+          "    }",
+          f"    mlc::store_pack<V>(out0 + o0 + ({it})cc * ({it}){Rn} + ({it})(q * V), o);",
+          "  }",
+          "}"]
+    grid = nb * rt_n * ct_n
+    spec = LaunchSpec("", grid, B, 0, {"kind": "transpose", "vec": V, "numel": k.numel,
+                                       "tile": T, "rows": Rn, "cols": Cn, "batches": nb,
+                                       "access": ["transpose"]})
+    return "\n".join(L), spec
+
+
 #: pointwise launch shape: threads per workgroup, and packs per thread once
 #: a launch has more than ``unroll_above`` packs
 POINTWISE_TUNING = {"block": 512, "unroll": 1, "unroll_above": 1 << 30}
@@ -1131,7 +1245,7 @@ def emit_kernel(k, cfg: Config) -> tuple[str, LaunchSpec] | None:
     """Source and launch spec of one kernel; ``None`` for an extern op that
     stays a library call."""
     if isinstance(k, PointwiseKernel):
-        return emit_pointwise(k, cfg)
+        return emit_transpose(k, cfg) or emit_pointwise(k, cfg)
     if isinstance(k, ReductionKernel):
         return emit_reduction(k, cfg)
     if isinstance(k, ExternKernel):
