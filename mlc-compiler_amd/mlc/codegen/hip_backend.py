@@ -633,24 +633,36 @@ def _prev_pow2(n: int) -> int:
     return 1 << (max(1, n).bit_length() - 1)
 
 
+#: persistent-reduction shape: packs each lane holds (the widest lane group
+#: with ``min_packs <= K <= max_packs`` wins) and the workgroup size cap
+REDUCTION_TUNING = {"min_packs": 2, "max_packs": 8, "block": 128}
+
+
 def reduction_geometry(n_rows: int, n_cols: int, V: int) -> dict:
     """Lanes per row G, packs per lane K, rows per workgroup."""
+    t = REDUCTION_TUNING
     nvec = -(-n_cols // V)
     G = None
-    if nvec <= WAVE * 8:
+    if nvec <= WAVE * t["max_packs"]:
         for g in (64, 32, 16, 8, 4, 2, 1):
-            if g <= nvec and nvec % g == 0 and nvec // g <= 8:
+            if g <= nvec and nvec % g == 0 and t["min_packs"] <= nvec // g <= t["max_packs"]:
                 G = g
                 break
+        if G is None:
+            for g in (64, 32, 16, 8, 4, 2, 1):
+                if g <= nvec and nvec % g == 0 and nvec // g <= t["max_packs"]:
+                    G = g
+                    break
         if G is None:
             G = min(WAVE, _prev_pow2(nvec))
     else:
         G = 128
-        while G < 1024 and -(-nvec // G) > 8:
+        while G < 1024 and -(-nvec // G) > t["max_packs"]:
             G *= 2
     K = -(-nvec // G)
     if G <= WAVE:
-        rows = max(WAVE // G, min(256 // G, max(1, -(-n_rows // 1024))))
+        cap = max(1, t["block"] // G)
+        rows = max(WAVE // G, min(cap, max(1, -(-n_rows // 1024))))
         rows = 1 << (rows.bit_length() - 1) if rows & (rows - 1) else rows
     else:
         rows = 1

@@ -10,8 +10,9 @@
 //    32-lane half) and v_readlane (the two 32-lane halves), giving every lane
 //    of the group the bit-identical result; groups wider than a wave combine
 //    per-wave partials through LDS in a fixed order;
-//  * scalar math helpers with torch semantics (NaN-propagating max/min, IEEE
-//    division, integer true division).
+//  * scalar math helpers with torch semantics (NaN-propagating max/min,
+//    correctly rounded division, integer true division); transcendentals
+//    are ROCm's device math library.
 //
 // No MFMA: every kernel generated here is HBM-bandwidth bound.
 #pragma once
@@ -120,6 +121,7 @@ __device__ __forceinline__ void store_pack(S* __restrict__ p, const R (&src)[V])
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float exp_(float x) { return expf(x); }
 __device__ __forceinline__ double exp_(double x) { return exp(x); }
+__device__ __forceinline__ float erf_(float x) { return erff(x); }
 __device__ __forceinline__ float log_(float x) { return logf(x); }
 __device__ __forceinline__ double log_(double x) { return log(x); }
 __device__ __forceinline__ float sqrt_(float x) { return sqrtf(x); }
@@ -132,7 +134,6 @@ __device__ __forceinline__ float cos_(float x) { return cosf(x); }
 __device__ __forceinline__ double cos_(double x) { return cos(x); }
 __device__ __forceinline__ float tanh_(float x) { return tanhf(x); }
 __device__ __forceinline__ double tanh_(double x) { return tanh(x); }
-__device__ __forceinline__ float erf_(float x) { return erff(x); }
 __device__ __forceinline__ double erf_(double x) { return erf(x); }
 __device__ __forceinline__ float sigmoid_(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ double sigmoid_(double x) { return 1.0 / (1.0 + exp(-x)); }

@@ -28,7 +28,7 @@ def flat_outputs(out):
 
 
 def lockstep(schedule, graph, params_cpu: dict, inputs_cpu, hip_runtime, check=None,
-             device="cuda"):
+             device="cuda", limit=None):
     """Run ``schedule`` twice in lockstep: the oracle on the CPU, and every
     generated kernel also through the HIP runtime on inputs copied from the
     oracle's buffers, so each kernel is compared on identical inputs.
@@ -43,10 +43,12 @@ def lockstep(schedule, graph, params_cpu: dict, inputs_cpu, hip_runtime, check=N
     cpu: dict[str, torch.Tensor] = {n: t.clone() for n, t in params_cpu.items()}
     for v, t in zip(graph.inputs, inputs_cpu):
         cpu[v.buffer.name] = t.reshape(-1).clone()
-    for b in graph.buffers():
-        if b.name not in cpu:
-            cpu[b.name] = torch.zeros(b.numel, dtype=b.dtype)
-    for k in schedule.kernels:
+    kernels = schedule.kernels if limit is None else schedule.kernels[:limit]
+    for k in kernels:
+        for v in list(k.reads()) + list(k.writes()):
+            if v.buffer.name not in cpu:
+                cpu[v.buffer.name] = torch.zeros(v.buffer.numel, dtype=v.buffer.dtype)
+    for k in kernels:
         names_in = {v.buffer.name for v in k.reads()}
         names_out = {v.buffer.name for v in k.writes()}
         gpu = {n: cpu[n].to(device) for n in names_in | names_out}
