@@ -15,6 +15,7 @@ from .config import Config
 from .ir.capture import capture
 from .kernels import Schedule
 from .lower import build_schedule
+from .passes.epilogue import fold_bias_epilogues
 from .passes.fusion import plan
 from .passes.memory_planning import plan_memory
 
@@ -40,6 +41,8 @@ def build_pipeline(graph, cfg: Config) -> Schedule:
     """Fusion, lowering to kernel IR and memory planning over a captured graph."""
     groups = plan(graph, cfg)
     schedule = build_schedule(graph, groups, cfg)
+    if cfg.gemm_epilogue:
+        fold_bias_epilogues(schedule)
     plan_memory(graph, schedule, cfg)
     return schedule
 

@@ -21,6 +21,10 @@ class Config:
     memory_planning: bool = True
     #: replay the schedule as one captured hipGraph
     cuda_graphs: bool = True
+    #: fold a bias add that would be a kernel of its own back into the GEMM
+    #: before it (addmm: hipBLASLt's bias epilogue). A schedule change, so it
+    #: is off by default, where the schedule is the reference's.
+    gemm_epilogue: bool = False
 
     # codegen
     pointwise_block: int = 1024

@@ -26,7 +26,9 @@ from . import native
 
 #: every (workload, config) pair a committed caller compiles
 DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()),
-           ("C5", Config()), ("C2", Config(max_persistent_row=64))]
+           ("C5", Config()), ("C2", Config(max_persistent_row=64)),
+           ("C2", Config(gemm_epilogue=True)), ("C3", Config(gemm_epilogue=True)),
+           ("C4", Config(gemm_epilogue=True))]
 
 
 def prebuild(items=None, verbose: bool = True) -> None:

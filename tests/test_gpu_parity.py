@@ -141,12 +141,15 @@ def test_transpose_template(shape, dtype):
 
 
 STREAMED64 = Config(max_persistent_row=64)
+EPILOGUE = Config(gemm_epilogue=True)
 
 
 @pytest.mark.parametrize("key,cfg,limit", [("C2", Config(), None), ("C3", Config(), None),
                                            ("C4", Config(), None), ("C2", STREAMED64, None),
-                                           ("C5", Config(), 16)],
-                         ids=["C2", "C3", "C4", "C2-streamed64", "C5-first-block"])
+                                           ("C5", Config(), 16), ("C2", EPILOGUE, None),
+                                           ("C3", EPILOGUE, None)],
+                         ids=["C2", "C3", "C4", "C2-streamed64", "C5-first-block",
+                              "C2-gemm-epilogue", "C3-gemm-epilogue"])
 def test_lockstep_every_kernel(key, cfg, limit):
     """Each generated kernel of the fp16 model, fed the oracle's own inputs:
     fp16 outputs within 2 ulp-scale (2e-3 relative to the largest magnitude),
@@ -182,8 +185,10 @@ def _truth_fp64(key):
         return flat_outputs(model(*args))
 
 
-@pytest.mark.parametrize("key", ["C2", "C3"])
-def test_end_to_end_fp16(key):
+@pytest.mark.parametrize("key,cfg", [("C2", Config()), ("C3", Config()), ("C2", EPILOGUE),
+                                     ("C3", EPILOGUE)],
+                         ids=["C2", "C3", "C2-gemm-epilogue", "C3-gemm-epilogue"])
+def test_end_to_end_fp16(key, cfg):
     """Free-running HIP model (hipGraph replay) end to end in fp16.
 
     Two fp16 implementations of a 12-layer model drift apart: wherever their
@@ -195,7 +200,6 @@ def test_end_to_end_fp16(key):
     GPU's extern results) must be no larger than eager PyTorch's.
     """
     model, args = make(key, "cpu")
-    cfg = Config()
     graph = capture(model, args)
     schedule = build_pipeline(graph, cfg)
     rt = HipRuntime(schedule, cfg, torch.device("cuda:0"))
@@ -261,6 +265,23 @@ def test_streamed_end_to_end(key):
     assert err <= 2e-3
     with torch.no_grad():
         torch.testing.assert_close(got.float(), gm(*ga).float(), rtol=1e-2, atol=5e-2)
+
+
+@pytest.mark.parametrize("key", ["C2", "C3"])
+def test_gemm_epilogue_matches_reference_schedule(key):
+    """The addmm-epilogue schedule computes the same function as the
+    reference schedule: outputs within one fp16 rounding of each other
+    (max relative error <= 2e-3); reports whether they are bit-identical."""
+    gm, ga = make(key, "cuda")
+    ref = flat_outputs(mlc.compile(gm, ga, Config())(*ga))[0].clone()
+    compiled = mlc.compile(gm, ga, EPILOGUE)
+    got = flat_outputs(compiled(*ga))[0]
+    torch.cuda.synchronize()
+    assert sum(1 for k in compiled.schedule.kernels if getattr(k, "node", None) is not None
+               and k.node.op == "aten.addmm.default") in (12, 36)
+    err = rel_err(got, ref)
+    print(key, "epilogue vs reference schedule: rel err", err, "bit-identical", torch.equal(got, ref))
+    assert err <= 2e-3
 
 
 def test_graph_replay_matches_plan_run():
