@@ -114,6 +114,45 @@ def test_device_exp_erf_error_bound(fn, lo, hi):
     assert err.max().item() <= 2.0
 
 
+class _Ragged(torch.nn.Module):
+    """Softmax, LayerNorm, variance and a GELU chain over awkward sizes."""
+
+    def __init__(self, d):
+        super().__init__()
+        self.ln = torch.nn.LayerNorm(d)
+
+    def forward(self, x, y):
+        a = (x * 0.3 + y).softmax(dim=-1)
+        b = self.ln(x + y)
+        v = x.var(dim=-1, keepdim=True, unbiased=False)
+        g = torch.nn.functional.gelu(x - y)
+        return a + b * v, g.amax(dim=-1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(3, 5, 100), (7, 50), (1, 1, 9), (5, 3, 1000), (2, 4099)])
+@pytest.mark.parametrize("cname", ["all_passes", "streamed"])
+def test_ragged_shapes(shape, dtype, cname):
+    """Sizes that are not multiples of the 16-byte pack, of the lanes per row
+    or of the rows per workgroup, so every tail and masked-lane path runs:
+    HIP against the oracle on the same inputs (fp32 at the reference's bar;
+    fp16/bf16 outputs within two storage roundings)."""
+    torch.manual_seed(0)
+    cfg = CONFIGS[cname]
+    x = torch.randn(*shape).to(dtype)
+    y = torch.randn(*shape).to(dtype)
+    model = _Ragged(shape[-1]).to(dtype)
+    want = compile_reference(model, (x, y), cfg)(x, y)
+    compiled = mlc.compile(model.cuda(), (x.cuda(), y.cuda()), cfg)
+    got = compiled(x.cuda(), y.cuda())
+    torch.cuda.synchronize()
+    for g, w in zip(flat_outputs(got), flat_outputs(want)):
+        if dtype == torch.float32:
+            torch.testing.assert_close(g.cpu(), w, rtol=1e-5, atol=1e-6)
+        else:
+            assert rel_err(g, w) <= (2e-3 if dtype == torch.float16 else 1.6e-2)
+
+
 class _TransposeBody(torch.nn.Module):
     def forward(self, x):
         return x.transpose(1, 2).contiguous() * 2.0 + 1.0
