@@ -158,15 +158,20 @@ def main() -> int:
         del compiled, model, inputs
         torch.cuda.empty_cache()
 
-    # SURVEY-ranked next row, measured beside the reference schedule: the GEMM
-    # bias epilogue (a different kernel schedule, so never the headline value)
+    # SURVEY-ranked next rows, measured beside the reference schedule: GEMM
+    # bias epilogues and layout selection (different kernel schedules, so
+    # never the headline value)
     variants = {}
-    for key in ("C2", "C4"):
+    for name, key, cfg in (("gemm_epilogue", "C2", Config(gemm_epilogue=True)),
+                           ("gemm_epilogue", "C4", Config(gemm_epilogue=True)),
+                           ("layout_selection", "C4", Config(layout_selection=True)),
+                           ("layout_selection+gemm_epilogue", "C4",
+                            Config(layout_selection=True, gemm_epilogue=True))):
         model, inputs = make(key, "cuda")
-        compiled = mlc.compile(model, inputs, Config(gemm_epilogue=True))
+        compiled = mlc.compile(model, inputs, cfg)
         r = _time_replays(compiled, inputs, opts.steps, opts.warmup)
-        variants[key] = {"ms_per_forward": round(r["ms_per_step"], 4),
-                         "kernels": compiled.schedule.counts()}
+        variants.setdefault(name, {})["b1" if key == "C2" else "b32"] = {
+            "ms_per_forward": round(r["ms_per_step"], 4), "kernels": compiled.schedule.counts()}
         del compiled, model, inputs
         torch.cuda.empty_cache()
 
@@ -209,7 +214,7 @@ def main() -> int:
                     **{k: results["C4"][k] for k in ("median_ms", "p10_ms", "kernels",
                                                      "graph_nodes", "arena_bytes")}},
         },
-        "gemm_epilogue_variant": {"b1": variants["C2"], "b32": variants["C4"]},
+        "schedule_variants": variants,
         "roofline": {
             "bound": "hbm",
             "kernel": f"{dom_sym}: {dom['kernel'].summary().split(': ', 1)[1]} (b32)",

@@ -17,6 +17,7 @@ from .kernels import Schedule
 from .lower import build_schedule
 from .passes.epilogue import fold_bias_epilogues
 from .passes.fusion import plan
+from .passes.layout import fold_relayout_copies
 from .passes.memory_planning import plan_memory
 
 
@@ -41,6 +42,8 @@ def build_pipeline(graph, cfg: Config) -> Schedule:
     """Fusion, lowering to kernel IR and memory planning over a captured graph."""
     groups = plan(graph, cfg)
     schedule = build_schedule(graph, groups, cfg)
+    if cfg.layout_selection:
+        fold_relayout_copies(schedule)
     if cfg.gemm_epilogue:
         fold_bias_epilogues(schedule)
     plan_memory(graph, schedule, cfg)

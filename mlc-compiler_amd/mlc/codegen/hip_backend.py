@@ -478,18 +478,28 @@ TRANSPOSE_BLOCK = 256
 def transpose_pattern(k: PointwiseKernel):
     """The batched 2-D transpose a pointwise kernel performs, if any.
 
-    Matches one input and one contiguous output where the output's fastest
-    dimension (``r``, size ``Rn``) is strided in the input (``Ri``), the
-    input's unit-stride dimension (``c``, size ``Cn``) sits directly outside it
-    in the output, and every other dimension is a whole ``Rn x Cn`` batch.
-    Returns (Rn, Cn, Ri, batches) or None.
+    Matches one contiguous output and one input (the *tiled* input) where the
+    output's fastest dimension (``r``, size ``Rn``) is strided in the input
+    (``Ri``), the input's unit-stride dimension (``c``, size ``Cn``) sits
+    directly outside it in the output, and every other dimension is a whole
+    ``Rn x Cn`` batch. Any other inputs must not vary along ``r`` (a bias
+    indexed by ``c``, say): they are read once per output row. Returns
+    (Rn, Cn, Ri, batches, tiled slot) or None.
     """
-    if len(k.inputs) != 1 or len(k.outputs) != 1:
+    if len(k.outputs) != 1:
         return None
-    out, inp = k.outputs[0], k.inputs[0]
+    out = k.outputs[0]
     if not (out.index.base == 0 and axis_terms(out.index, "idx") == ((k.numel, 1, 1),)):
         return None
-    if inp.dtype != out.dtype or inp.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+    if out.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return None
+    tiled = [i for i, a in enumerate(k.inputs)
+             if any(t[1] == 1 for t in axis_terms(a.index, "idx"))]
+    if len(tiled) != 1:
+        return None
+    slot = tiled[0]
+    inp = k.inputs[slot]
+    if inp.dtype not in (torch.float16, torch.bfloat16, torch.float32):
         return None
     terms = axis_terms(inp.index, "idx")
     r = [t for t in terms if t[1] == 1]
@@ -507,34 +517,44 @@ def transpose_pattern(k: PointwiseKernel):
     if Rn % T or Cn % T:
         return None
     V = 16 // itemsize(inp.dtype)
+    if 16 // itemsize(out.dtype) != V:
+        return None
     others = [t[2] for t in terms if t is not r[0] and t is not c[0]]
     if inp.index.base % V or Ri % V or any(o % V for o in others):
         return None
-    return Rn, Cn, Ri, k.numel // plane
+    return Rn, Cn, Ri, k.numel // plane, slot
 
 
 def emit_transpose(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, LaunchSpec] | None:
-    """A batched transpose copy (with its elementwise body) staged through
-    LDS in 64x64 tiles: 128-bit loads along the input's contiguous dimension,
-    128-bit stores along the output's, so neither side gathers."""
+    """A batched transpose (with its elementwise body) staged through LDS in
+    64x64 tiles: 128-bit loads along the tiled input's contiguous dimension,
+    128-bit stores along the output's, so neither side gathers. Inputs that
+    are constant along the output's fast dimension load once per output row."""
     pat = transpose_pattern(k)
     if pat is None:
         return None
-    Rn, Cn, Ri, nb = pat
+    Rn, Cn, Ri, nb, slot = pat
     T, B = TRANSPOSE_TILE, TRANSPOSE_BLOCK
-    inp, out = k.inputs[0], k.outputs[0]
+    inp, out = k.inputs[slot], k.outputs[0]
     S = STORAGE[inp.dtype]
     V = 16 // itemsize(inp.dtype)
     it = index_type(k)
     W = T + 2  # LDS row pitch: the transposed gather hits distinct banks
     per_thread = (T * T // V) // B
-    in_parts = render_terms(axis_terms(inp.index, "idx"), k.numel, "o0", it)
-    if inp.index.base:
-        in_parts.append(f"({it}){inp.index.base}")
-    in_off = join_offset(in_parts, it)
-    ct = compute_type(inp.dtype)
+
+    def offset_at(a, var: str) -> str:
+        parts = render_terms(axis_terms(a.index, "idx"), k.numel, var, it)
+        if a.index.base:
+            parts.append(f"({it}){a.index.base}")
+        return join_offset(parts, it)
+
+    in_types = [compute_type(a.dtype) for a in k.inputs]
     temp_types: dict[str, str] = {}
-    r = Renderer(lambda slot: ("x0", ct), lambda n: (n, temp_types[n]))
+
+    def operand(s_: int):
+        return ("x0" if s_ == slot else f"xr{s_}"), in_types[s_]
+
+    r = Renderer(operand, lambda n: (n, temp_types[n]))
     body = []
     for name, expr in k.body:
         code, t = r(expr)
@@ -553,13 +573,13 @@ def emit_transpose(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
          f"  const {it} c0 = ((t / ({it}){rt_n}) % ({it}){ct_n}) * T;",
          f"  const {it} b = t / ({it}){rt_n * ct_n};",
          f"  const {it} o0 = b * ({it}){Rn * Cn} + c0 * ({it}){Rn} + r0;",
-         f"  const {it} i0 = {in_off};",
+         f"  const {it} i0 = {offset_at(inp, 'o0')};",
          "#pragma unroll",
          f"  for (int u = 0; u < {per_thread}; ++u) {{",
          f"    const int id = u * {B} + (int)threadIdx.x;",
          "    const int rr = id / (T / V), p = id % (T / V);",
          f"    const mlc::pack<{S}, V> w = *reinterpret_cast<const mlc::pack<{S}, V>*>("
-         f"in0 + i0 + ({it})rr * ({it}){Ri} + ({it})(p * V));",
+         f"in{slot} + i0 + ({it})rr * ({it}){Ri} + ({it})(p * V));",
          "#pragma unroll",
          "    for (int j = 0; j < V; ++j) tile[rr * W + p * V + j] = w.x[j];",
          "  }",
@@ -567,11 +587,15 @@ def emit_transpose(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
          "#pragma unroll",
          f"  for (int u = 0; u < {per_thread}; ++u) {{",
          f"    const int id = u * {B} + (int)threadIdx.x;",
-         "    const int cc = id / (T / V), q = id % (T / V);",
-         f"    {compute_type_of_out(k, out)} o[V];",
-         "#pragma unroll",
-         "    for (int j = 0; j < V; ++j) {",
-         "      const auto x0 = mlc::ld(&tile[(q * V + j) * W + cc]);"]
+         "    const int cc = id / (T / V), q = id % (T / V);"]
+    for s_, a in enumerate(k.inputs):
+        if s_ != slot:
+            L.append(f"    const {it} oc{s_} = o0 + ({it})cc * ({it}){Rn};")
+            L.append(f"    const {in_types[s_]} xr{s_} = mlc::ld(in{s_} + {offset_at(a, f'oc{s_}')});")
+    L += [f"    {compute_type_of_out(k, out)} o[V];",
+          "#pragma unroll",
+          "    for (int j = 0; j < V; ++j) {",
+          "      const auto x0 = mlc::ld(&tile[(q * V + j) * W + cc]);"]
     L += body
     L += [f"      o[j] = {oc};",
           "    }",

@@ -25,6 +25,10 @@ class Config:
     #: before it (addmm: hipBLASLt's bias epilogue). A schedule change, so it
     #: is off by default, where the schedule is the reference's.
     gemm_epilogue: bool = False
+    #: merge a pointwise producer into the copy that re-lays its output out
+    #: (q/k/v written straight in the bmm layout). A schedule change, off by
+    #: default.
+    layout_selection: bool = False
 
     # codegen
     pointwise_block: int = 1024

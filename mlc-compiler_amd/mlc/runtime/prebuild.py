@@ -28,7 +28,9 @@ from . import native
 DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()),
            ("C5", Config()), ("C2", Config(max_persistent_row=64)),
            ("C2", Config(gemm_epilogue=True)), ("C3", Config(gemm_epilogue=True)),
-           ("C4", Config(gemm_epilogue=True))]
+           ("C4", Config(gemm_epilogue=True)), ("C4", Config(layout_selection=True)),
+           ("C5", Config(layout_selection=True)),
+           ("C4", Config(layout_selection=True, gemm_epilogue=True))]
 
 
 def prebuild(items=None, verbose: bool = True) -> None:

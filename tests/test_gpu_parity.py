@@ -181,14 +181,17 @@ def test_transpose_template(shape, dtype):
 
 STREAMED64 = Config(max_persistent_row=64)
 EPILOGUE = Config(gemm_epilogue=True)
+LAYOUT = Config(layout_selection=True)
 
 
 @pytest.mark.parametrize("key,cfg,limit", [("C2", Config(), None), ("C3", Config(), None),
                                            ("C4", Config(), None), ("C2", STREAMED64, None),
                                            ("C5", Config(), 16), ("C2", EPILOGUE, None),
-                                           ("C3", EPILOGUE, None)],
+                                           ("C3", EPILOGUE, None), ("C4", LAYOUT, None),
+                                           ("C5", LAYOUT, 14)],
                          ids=["C2", "C3", "C4", "C2-streamed64", "C5-first-block",
-                              "C2-gemm-epilogue", "C3-gemm-epilogue"])
+                              "C2-gemm-epilogue", "C3-gemm-epilogue", "C4-layout",
+                              "C5-layout-first-block"])
 def test_lockstep_every_kernel(key, cfg, limit):
     """Each generated kernel of the fp16 model, fed the oracle's own inputs:
     fp16 outputs within 2 ulp-scale (2e-3 relative to the largest magnitude),
@@ -321,6 +324,22 @@ def test_gemm_epilogue_matches_reference_schedule(key):
     err = rel_err(got, ref)
     print(key, "epilogue vs reference schedule: rel err", err, "bit-identical", torch.equal(got, ref))
     assert err <= 2e-3
+
+
+@pytest.mark.parametrize("key", ["C4", "C5"])
+def test_layout_selection_matches_reference_schedule(key):
+    """Layout selection merges producers into the copies that re-lay them
+    out; the arithmetic is unchanged, so outputs are bit-identical to the
+    reference schedule's, at full size."""
+    gm, ga = make(key, "cuda")
+    ref = flat_outputs(mlc.compile(gm, ga, Config())(*ga))[0].clone()
+    compiled = mlc.compile(gm, ga, LAYOUT)
+    kinds = [s.meta["kind"] for s in compiled._module.launch_table.values()]
+    assert kinds.count("transpose") == 12
+    got = flat_outputs(compiled(*ga))[0]
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    del ref, got, compiled
 
 
 def test_graph_replay_matches_plan_run():
