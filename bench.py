@@ -158,6 +158,7 @@ def main() -> int:
         del compiled, model, inputs
         torch.cuda.empty_cache()
 
+    FAST = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True)
     # SURVEY-ranked next rows, measured beside the reference schedule: GEMM
     # bias epilogues and layout selection (different kernel schedules, so
     # never the headline value)
@@ -166,7 +167,9 @@ def main() -> int:
                            ("gemm_epilogue", "C4", Config(gemm_epilogue=True)),
                            ("layout_selection", "C4", Config(layout_selection=True)),
                            ("layout_selection+gemm_epilogue", "C4",
-                            Config(layout_selection=True, gemm_epilogue=True))):
+                            Config(layout_selection=True, gemm_epilogue=True)),
+                           ("all: merged qkv GEMM+epilogue+layout", "C2", FAST),
+                           ("all: merged qkv GEMM+epilogue+layout", "C4", FAST)):
         model, inputs = make(key, "cuda")
         compiled = mlc.compile(model, inputs, cfg)
         r = _time_replays(compiled, inputs, opts.steps, opts.warmup)

@@ -17,6 +17,7 @@ from .kernels import Schedule
 from .lower import build_schedule
 from .passes.epilogue import fold_bias_epilogues
 from .passes.fusion import plan
+from .passes.horizontal import merge_parallel_gemms
 from .passes.layout import fold_relayout_copies
 from .passes.memory_planning import plan_memory
 
@@ -40,6 +41,8 @@ def compile(model: torch.nn.Module, example_inputs: Sequence[torch.Tensor],
 
 def build_pipeline(graph, cfg: Config) -> Schedule:
     """Fusion, lowering to kernel IR and memory planning over a captured graph."""
+    if cfg.merge_parallel_gemms:
+        merge_parallel_gemms(graph)
     groups = plan(graph, cfg)
     schedule = build_schedule(graph, groups, cfg)
     if cfg.layout_selection:

@@ -29,6 +29,9 @@ class Config:
     #: (q/k/v written straight in the bmm layout). A schedule change, off by
     #: default.
     layout_selection: bool = False
+    #: merge linear layers that read the same activation (BERT's q/k/v) into
+    #: one GEMM over concatenated weights. A graph rewrite, off by default.
+    merge_parallel_gemms: bool = False
 
     # codegen
     pointwise_block: int = 1024

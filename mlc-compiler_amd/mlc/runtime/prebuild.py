@@ -24,13 +24,16 @@ from ..config import Config
 from ..ir.capture import capture
 from . import native
 
+FAST = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True)
+
 #: every (workload, config) pair a committed caller compiles
 DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()),
            ("C5", Config()), ("C2", Config(max_persistent_row=64)),
            ("C2", Config(gemm_epilogue=True)), ("C3", Config(gemm_epilogue=True)),
            ("C4", Config(gemm_epilogue=True)), ("C4", Config(layout_selection=True)),
            ("C5", Config(layout_selection=True)),
-           ("C4", Config(layout_selection=True, gemm_epilogue=True))]
+           ("C4", Config(layout_selection=True, gemm_epilogue=True)),
+           ("C2", FAST), ("C4", FAST)]
 
 
 def prebuild(items=None, verbose: bool = True) -> None:

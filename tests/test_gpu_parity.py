@@ -182,16 +182,18 @@ def test_transpose_template(shape, dtype):
 STREAMED64 = Config(max_persistent_row=64)
 EPILOGUE = Config(gemm_epilogue=True)
 LAYOUT = Config(layout_selection=True)
+FAST = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True)
 
 
 @pytest.mark.parametrize("key,cfg,limit", [("C2", Config(), None), ("C3", Config(), None),
                                            ("C4", Config(), None), ("C2", STREAMED64, None),
                                            ("C5", Config(), 16), ("C2", EPILOGUE, None),
                                            ("C3", EPILOGUE, None), ("C4", LAYOUT, None),
-                                           ("C5", LAYOUT, 14)],
+                                           ("C5", LAYOUT, 14), ("C2", FAST, None),
+                                           ("C4", FAST, None)],
                          ids=["C2", "C3", "C4", "C2-streamed64", "C5-first-block",
                               "C2-gemm-epilogue", "C3-gemm-epilogue", "C4-layout",
-                              "C5-layout-first-block"])
+                              "C5-layout-first-block", "C2-all-variants", "C4-all-variants"])
 def test_lockstep_every_kernel(key, cfg, limit):
     """Each generated kernel of the fp16 model, fed the oracle's own inputs:
     fp16 outputs within 2 ulp-scale (2e-3 relative to the largest magnitude),
@@ -228,8 +230,9 @@ def _truth_fp64(key):
 
 
 @pytest.mark.parametrize("key,cfg", [("C2", Config()), ("C3", Config()), ("C2", EPILOGUE),
-                                     ("C3", EPILOGUE)],
-                         ids=["C2", "C3", "C2-gemm-epilogue", "C3-gemm-epilogue"])
+                                     ("C3", EPILOGUE), ("C2", FAST)],
+                         ids=["C2", "C3", "C2-gemm-epilogue", "C3-gemm-epilogue",
+                              "C2-all-variants"])
 def test_end_to_end_fp16(key, cfg):
     """Free-running HIP model (hipGraph replay) end to end in fp16.
 
