@@ -80,6 +80,22 @@ def _kernel_table(compiled, iters: int):
     return rows
 
 
+def _attention_row(compiled, iters: int) -> dict:
+    """Average launch time and algorithmic bandwidth of the fused attention
+    kernel (every layer shares one function)."""
+    from mlc.bench.roofline import HBM_PEAK_GBS
+    from mlc.kernels import AttentionKernel
+
+    rows = [r for r in _kernel_table(compiled, iters) if isinstance(r[0], AttentionKernel)]
+    if not rows:
+        return {}
+    ms = statistics.mean(r[3] for r in rows)
+    gbs = rows[0][2] / (ms * 1e-3) / 1e9
+    return {"symbol": rows[0][1], "launch_us": round(ms * 1e3, 3),
+            "bytes_per_launch": rows[0][2], "achieved_gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def _measured_traffic(symbol: str):
     """Counter-measured HBM bytes per launch of ``symbol`` from the committed
     PMC summary (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a
@@ -159,6 +175,9 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     FAST = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True)
+    ATTENTION = Config(fused_attention=True)
+    ALL = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True,
+                 fused_attention=True)
     # SURVEY-ranked next rows, measured beside the reference schedule: GEMM
     # bias epilogues and layout selection (different kernel schedules, so
     # never the headline value)
@@ -169,12 +188,19 @@ def main() -> int:
                            ("layout_selection+gemm_epilogue", "C4",
                             Config(layout_selection=True, gemm_epilogue=True)),
                            ("all: merged qkv GEMM+epilogue+layout", "C2", FAST),
-                           ("all: merged qkv GEMM+epilogue+layout", "C4", FAST)):
+                           ("all: merged qkv GEMM+epilogue+layout", "C4", FAST),
+                           ("fused_attention", "C2", ATTENTION),
+                           ("fused_attention", "C4", ATTENTION),
+                           ("all + fused_attention", "C2", ALL),
+                           ("all + fused_attention", "C4", ALL)):
         model, inputs = make(key, "cuda")
         compiled = mlc.compile(model, inputs, cfg)
         r = _time_replays(compiled, inputs, opts.steps, opts.warmup)
-        variants.setdefault(name, {})["b1" if key == "C2" else "b32"] = {
-            "ms_per_forward": round(r["ms_per_step"], 4), "kernels": compiled.schedule.counts()}
+        entry = {"ms_per_forward": round(r["ms_per_step"], 4),
+                 "kernels": compiled.schedule.counts()}
+        if cfg.fused_attention:
+            entry["attention_kernel"] = _attention_row(compiled, opts.kernel_iters)
+        variants.setdefault(name, {})["b1" if key == "C2" else "b32"] = entry
         del compiled, model, inputs
         torch.cuda.empty_cache()
 

@@ -15,6 +15,7 @@ from .config import Config
 from .ir.capture import capture
 from .kernels import Schedule
 from .lower import build_schedule
+from .passes.attention import fuse_attention
 from .passes.epilogue import fold_bias_epilogues
 from .passes.fusion import plan
 from .passes.horizontal import merge_parallel_gemms
@@ -49,6 +50,8 @@ def build_pipeline(graph, cfg: Config) -> Schedule:
         fold_relayout_copies(schedule)
     if cfg.gemm_epilogue:
         fold_bias_epilogues(schedule)
+    if cfg.fused_attention:
+        fuse_attention(schedule)
     plan_memory(graph, schedule, cfg)
     return schedule
 

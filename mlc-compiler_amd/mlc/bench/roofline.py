@@ -8,7 +8,10 @@ roofline is priced in.
 An index map's distinct elements are the product of the sizes of its
 canonical terms (stride-0 dims are already dropped, so a broadcast operand
 counts once). This equals the reference cost model's traffic
-(``mlc/passes/cost.py:44-59``) when no operand is broadcast-expanded.
+(``mlc/passes/cost.py:44-59``) when no operand is broadcast-expanded. A fused
+attention kernel is priced the same way: q, k, v and the reduction's other
+operands read once, the output written once (the scores and probabilities it
+keeps on chip are not HBM traffic).
 """
 
 from __future__ import annotations
@@ -18,7 +21,7 @@ import math
 import torch
 
 from ..codegen.index import IndexMap
-from ..kernels import ExternKernel, PointwiseKernel, ReductionKernel
+from ..kernels import AttentionKernel, ExternKernel, PointwiseKernel, ReductionKernel
 
 #: MI355X published peak HBM3E bandwidth, GB/s
 HBM_PEAK_GBS = 8000.0
@@ -39,7 +42,7 @@ def algorithmic_bytes(k) -> int:
             ids = k.node.args[1]
             return 2 * out.numel * _itemsize(out.dtype) + ids.numel * _itemsize(ids.dtype)
         raise TypeError(f"no byte model for extern {k.node.op}")
-    if not isinstance(k, (PointwiseKernel, ReductionKernel)):
+    if not isinstance(k, (PointwiseKernel, ReductionKernel, AttentionKernel)):
         raise TypeError(type(k).__name__)
     seen = set()
     total = 0

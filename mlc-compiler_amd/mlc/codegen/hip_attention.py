@@ -1,0 +1,333 @@
+"""HIP emitter for :class:`~mlc.kernels.AttentionKernel` (gfx950 MFMA).
+
+One workgroup of ``W`` waves per (batch-head, block of ``16*W`` queries):
+
+* **staging**: the block's queries, and every key and value of the head,
+  are copied from their strided views into LDS with 128-bit loads along
+  whichever axis is unit-stride, all loads issued before the first LDS
+  store. K is kept as ``[key][d]`` and V transposed
+  as ``[d][key]``; row pitches are padded by 8 halfs so the 16-lane phases of
+  ``ds_read_b128`` hit distinct banks.
+* **scores**: each wave owns 16 queries and computes ``S^T = K Q^T`` with
+  ``v_mfma_f32_16x16x32_f16`` -- A = a 16-key tile of K, B = the wave's Q
+  fragment (read once) -- so lane ``l`` ends up holding query ``l % 16``'s
+  scores for keys ``16 t + 4 (l / 16) + i``. Scores are rounded to their
+  storage dtype, as the unfused schedule stores them.
+* **row reduction**: the reduction kernel's own steps are rendered per
+  element; each query's row lives in four lanes (``l % 16`` fixed), so a
+  reduce is a lane-local loop plus two ``__shfl_xor`` (16, 32).
+* **values**: ``O^T = V^T P^T`` on the same MFMA. The score layout of lane
+  ``l`` is exactly the B fragment of ``P^T`` when the 32-element k axis of an
+  MFMA pairs two 16-key tiles, so probabilities never leave registers; A is
+  read from the transposed V tile with two ``ds_read_b64``. Lane ``l`` ends
+  with four consecutive head-dim values of query ``l % 16``: one 8-byte
+  store each.
+
+Numerics follow the unfused schedule: fp32 accumulation, scores and
+probabilities rounded to their storage dtypes before use, fp32 softmax.
+Summation orders differ from the library GEMMs and from the standalone
+reduction kernel, so results agree to rounding, not bit for bit.
+"""
+
+from __future__ import annotations
+
+from ..kernels import AttentionKernel, Bind
+from .hip_backend import (_IDENTITY, _OP, WAVE, LaunchSpec, Renderer, _RowOffsets,
+                          _expr_varies, _params, _reciprocal_divisors, _reciprocal_lines,
+                          _row_col_access, _scalar_division, cast_code,
+                          compute_type, index_type)
+from .reduction_schedule import varies_by_column
+
+#: waves per workgroup (each owns 16 queries): ``waves`` forces a count;
+#: otherwise the largest of ``choices`` that still gives ``min_workgroups``
+#: workgroups (one per CU), else the smallest. Measured on MI355X for BERT's
+#: 128 x 128 x 64 heads: 12 heads -> 2 waves (5.3 us vs 5.7 at 4 and 7.0 at
+#: 8); 384 heads -> 8 waves (12.6 us vs 14.8 at 4, 18.3 at 2).
+ATTENTION_TUNING = {"waves": None, "choices": (8, 4, 2), "min_workgroups": 256}
+
+
+def attention_waves(heads: int, queries: int) -> int:
+    forced = ATTENTION_TUNING["waves"]
+    if forced:
+        return max(1, min(forced, queries // 16))
+    choices = [w for w in ATTENTION_TUNING["choices"] if 16 * w <= max(16, queries)] or [1]
+    for w in choices:
+        if heads * -(-queries // (16 * w)) >= ATTENTION_TUNING["min_workgroups"]:
+            return w
+    return choices[-1]
+
+
+def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc: int, pr: int,
+           pc: int, aligned_c: bool, aligned_r: bool, threads: int, rows_valid: str | None,
+           it: str) -> tuple[list[str], list[str]]:
+    """Copy the R x C tile ``src[base + r*sr + c*sc]`` to ``lds[r*pr + c*pc]``.
+
+    Returns (load lines, store lines): every load of every operand is issued
+    before the first LDS store, so the workgroup waits for memory once, not
+    once per loop trip."""
+    load: list[str] = []
+    store: list[str] = []
+    if sc == 1 and C % 8 == 0 and aligned_c:
+        mode, per = "c", 8
+    elif sr == 1 and R % 8 == 0 and aligned_r and not rows_valid:
+        mode, per = "r", 8
+    else:
+        mode, per = "s", 1
+    n = R * C // per
+    trips = -(-n // threads)
+    full = n % threads == 0
+    ty = "mlc::f16x8" if per == 8 else "mlc::f16"
+    load.append(f"  {ty} {tag}[{trips}];")
+    load.append("#pragma unroll")
+    load.append(f"  for (int u = 0; u < {trips}; ++u) {{")
+    load.append(f"    const int e = (int)threadIdx.x + u * {threads};")
+    store.append("#pragma unroll")
+    store.append(f"  for (int u = 0; u < {trips}; ++u) {{")
+    store.append(f"    const int e = (int)threadIdx.x + u * {threads};")
+    conds = [] if full else [f"e < {n}"]
+    if mode == "c":
+        rc = f"const int r = e / {C // 8}, c = (e % {C // 8}) * 8;"
+        addr = f"{src} + {base} + ({it})r * ({it}){sr} + ({it})c"
+    elif mode == "r":
+        rc = f"const int c = e / {R // 8}, r = (e % {R // 8}) * 8;"
+        addr = f"{src} + {base} + ({it})r + ({it})c * ({it}){sc}"
+    else:
+        rc = f"const int r = e / {C}, c = e % {C};"
+        addr = None
+    if rows_valid:
+        conds.append(f"r < {rows_valid}")
+    guard = f"if ({' && '.join(conds)}) " if conds else ""
+    load.append(f"    {rc}")
+    store.append(f"    {rc}")
+    if per == 8:
+        load.append(f"    {guard}{tag}[u] = *reinterpret_cast<const mlc::f16x8*>({addr});")
+        if mode == "c" and pc == 1 and pr % 8 == 0:
+            store.append(f"    {guard}*reinterpret_cast<mlc::f16x8*>({lds} + r * {pr} + c) = {tag}[u];")
+        elif mode == "r" and pr == 1 and pc % 8 == 0:
+            store.append(f"    {guard}*reinterpret_cast<mlc::f16x8*>({lds} + r + c * {pc}) = {tag}[u];")
+        else:
+            step_r, step_c = (0, 1) if mode == "c" else (1, 0)
+            store.append(f"    {guard}{{")
+            store.append("#pragma unroll")
+            store.append(f"      for (int j = 0; j < 8; ++j) {lds}[(r + j * {step_r}) * {pr} + "
+                         f"(c + j * {step_c}) * {pc}] = {tag}[u].v[j];")
+            store.append("    }")
+    else:
+        load.append(f"    {guard}{tag}[u] = {src}[{base} + ({it})r * ({it}){sr} + ({it})c * ({it}){sc}];")
+        store.append(f"    {guard}{lds}[r * {pr} + c * {pc}] = {tag}[u];")
+    load.append("  }")
+    store.append("  }")
+    return load, store
+
+
+def _aligned(offset: int, strides) -> bool:
+    return offset % 8 == 0 and all(s % 8 == 0 for s in strides)
+
+
+def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
+    sm = k.softmax
+    BH, T, D = k.q.shape
+    Tk = k.kt.shape[2]
+    NT = Tk // 16
+    W = attention_waves(BH, T)
+    QB = 16 * W
+    NQB = -(-T // QB)
+    THREADS = W * WAVE
+    it = index_type(k)
+    PK, PV, PQ = D + 8, Tk + 8, D + 8
+    lds_bytes = 2 * (Tk * PK + D * PV + QB * PQ)
+
+    L: list[str] = []
+    L.append(f"extern \"C\" __global__ void __launch_bounds__({THREADS}) "
+             f"KERNEL({', '.join(_params(k))}) {{")
+    L.append(f"  // attention: {BH} heads x [{T} x {D}] x [{Tk}]; {QB} queries per workgroup, "
+             f"16 per wave")
+    L.append(f"  __shared__ __align__(16) mlc::f16 ks[{Tk * PK}];")
+    L.append(f"  __shared__ __align__(16) mlc::f16 vt[{D * PV}];")
+    L.append(f"  __shared__ __align__(16) mlc::f16 qs[{QB * PQ}];")
+    L.append(f"  const {it} bh = ({it})(blockIdx.x / {NQB});")
+    L.append(f"  const int q0 = (int)(blockIdx.x % {NQB}) * {QB};")
+
+    ql_ = k.q.layout
+    qsb, qsr, qsc = ql_.strides
+    rows_valid = None
+    if T % QB:
+        L.append(f"  const int qn = {T} - q0 < {QB} ? {T} - q0 : {QB};")
+        rows_valid = "qn"
+    q_ld, q_st = _stage("gq", "qs", "in0",
+                        f"(({it}){ql_.offset} + bh * ({it}){qsb} + ({it})q0 * ({it}){qsr})",
+                        QB, D, qsr, qsc, PQ, 1, _aligned(ql_.offset, (qsb, qsr)),
+                        _aligned(ql_.offset, (qsb, qsc)), THREADS, rows_valid, it)
+    # kt is [BH, D, Tk]: key r, dim c sits at r*sk + c*sd
+    kl = k.kt.layout
+    ksb, ksd, ksk = kl.strides
+    k_ld, k_st = _stage("gk", "ks", "in1", f"(({it}){kl.offset} + bh * ({it}){ksb})", Tk, D, ksk,
+                        ksd, PK, 1, _aligned(kl.offset, (ksb, ksk)),
+                        _aligned(kl.offset, (ksb, ksd)), THREADS, None, it)
+    # v is [BH, Tk, D], staged transposed as [d][key]
+    vl = k.v.layout
+    vsb, vsk, vsd = vl.strides
+    v_ld, v_st = _stage("gv", "vt", "in2", f"(({it}){vl.offset} + bh * ({it}){vsb})", Tk, D, vsk,
+                        vsd, 1, PV, _aligned(vl.offset, (vsb, vsk)),
+                        _aligned(vl.offset, (vsb, vsd)), THREADS, None, it)
+    L += q_ld + k_ld + v_ld + q_st + k_st + v_st
+    L.append("  __syncthreads();")
+    L.append("  const int w = threadIdx.x / 64, l = threadIdx.x % 64;")
+    L.append("  const int ql = l % 16, g = l / 16;")
+    L.append("  const int qw = q0 + w * 16;")
+    L.append(f"  if (qw >= {T}) return;  // no barrier follows")
+    # scores
+    L.append(f"  mlc::half8 qf[{D // 32}];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int dc = 0; dc < {D // 32}; ++dc)")
+    L.append(f"    qf[dc] = *reinterpret_cast<const mlc::half8*>(qs + (w * 16 + ql) * {PQ} + dc * 32 + g * 8);")
+    L.append(f"  float s[{NT}][4];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int t = 0; t < {NT}; ++t) {{")
+    L.append("    mlc::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};")
+    L.append("#pragma unroll")
+    L.append(f"    for (int dc = 0; dc < {D // 32}; ++dc) {{")
+    L.append(f"      const mlc::half8 kf = *reinterpret_cast<const mlc::half8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
+    L.append("      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[dc], acc, 0, 0, 0);")
+    L.append("    }")
+    L.append("#pragma unroll")
+    L.append(f"    for (int i = 0; i < 4; ++i) s[t][i] = {cast_code('acc[i]', k.score_dtype)[0]};")
+    L.append("  }")
+    L.append(f"  const {it} row = bh * ({it}){T} + ({it})(qw + ql);")
+
+    # the reduction's other operands
+    offs = _RowOffsets(sm, it)
+    vector = varies_by_column(sm)
+    col_slots = [i for i, a in enumerate(sm.inputs) if a.index.varies_along("col")]
+    param = {}
+    n = 3
+    for i in range(len(sm.inputs)):
+        if i != k.score_slot:
+            param[i] = n
+            n += 1
+    in_types = {i: compute_type(a.dtype) for i, a in enumerate(sm.inputs)}
+    for i, a in enumerate(sm.inputs):
+        if i == k.score_slot:
+            continue
+        p, ct = param[i], in_types[i]
+        if i not in col_slots:
+            L.append(f"  const {ct} x{i} = mlc::ld(in{p} + {offs.row(a)});")
+            continue
+        acc = _row_col_access(sm, a, 4)
+        L.append(f"  {ct} x{i}[{NT}][4];")
+        L.append(f"  {{ const {it} rb = {offs.row(a)};")
+        L.append("#pragma unroll")
+        L.append(f"    for (int t = 0; t < {NT}; ++t) {{")
+        L.append(f"      const {it} c0 = ({it})(t * 16 + g * 4);")
+        if acc.mode == "affine" and acc.aligned:
+            L.append(f"      mlc::load_pack<4>(x{i}[t], in{p} + rb + {offs.col(a, 'c0')});")
+        else:
+            L.append("#pragma unroll")
+            L.append(f"      for (int j = 0; j < 4; ++j) x{i}[t][j] = "
+                     f"mlc::ld(in{p} + rb + {offs.col(a, '(c0 + (' + it + ')j)')});")
+        L.append("    }")
+        L.append("  }")
+
+    temp_types: dict[str, str] = {}
+
+    def ref_elem(slot):
+        if slot == k.score_slot:
+            return "s[t][i]", "float"
+        if slot in col_slots:
+            return f"x{slot}[t][i]", in_types[slot]
+        return f"x{slot}", in_types[slot]
+
+    def ref_scalar(slot):
+        if slot == k.score_slot or slot in col_slots:
+            raise AssertionError("column operand read in a row-scalar expression")
+        return f"x{slot}", in_types[slot]
+
+    def temp_elem(name):
+        return (f"{name}[t][i]" if name in vector else name), temp_types[name]
+
+    def temp_scalar(name):
+        if name in vector:
+            raise AssertionError("vector temp read in a row-scalar expression")
+        return name, temp_types[name]
+
+    elem_r = Renderer(ref_elem, temp_elem)
+    scal_r = Renderer(ref_scalar, temp_scalar)
+    rcp_for = _reciprocal_divisors(sm, vector)
+    score_cols = set(col_slots) | {k.score_slot}
+
+    def elem_loop(target: str, code: str) -> list[str]:
+        return ["#pragma unroll", f"  for (int t = 0; t < {NT}; ++t)", "#pragma unroll",
+                "    for (int i = 0; i < 4; ++i)", f"      {target}[t][i] = {code};"]
+
+    for st in sm.steps:
+        if isinstance(st, Bind):
+            if st.name in vector:
+                code, t = elem_r(st.expr)
+                temp_types[st.name] = t
+                L.append(f"  {t} {st.name}[{NT}][4];")
+                sd = _scalar_division(st.expr, rcp_for)
+                if sd is not None and t == "float":
+                    num, d = elem_r(sd[0])[0], sd[1]
+                    L.append(f"  if (__all(ok_{d})) {{")
+                    L += elem_loop(st.name, f"mlc::div_rcp({num}, {d}, rcp_{d})")
+                    L.append("  } else {")
+                    L += elem_loop(st.name, code)
+                    L.append("  }")
+                else:
+                    L += elem_loop(st.name, code)
+            else:
+                code, t = scal_r(st.expr)
+                temp_types[st.name] = t
+                L.append(f"  const {t} {st.name} = {code};")
+                L += _reciprocal_lines(st.name, rcp_for)
+            continue
+        code, t = elem_r(st.expr) if _expr_varies(st.expr, score_cols, vector) else scal_r(st.expr)
+        if t == "bool":
+            code, t = f"((int64_t)({code}))", "int64_t"
+        temp_types[st.name] = t
+        op = _OP[st.kind]
+        L.append(f"  {t} {st.name};")
+        L.append("  {")
+        L.append(f"    {t} acc = {_IDENTITY[st.kind][t]};")
+        L.append("#pragma unroll")
+        L.append(f"    for (int t = 0; t < {NT}; ++t)")
+        L.append("#pragma unroll")
+        L.append(f"      for (int i = 0; i < 4; ++i) acc = {op}::f(acc, ({t})({code}));")
+        L.append(f"    acc = {op}::f(acc, __shfl_xor(acc, 16, 64));")
+        L.append(f"    acc = {op}::f(acc, __shfl_xor(acc, 32, 64));")
+        L.append(f"    {st.name} = acc;")
+        L.append("  }")
+        L += _reciprocal_lines(st.name, rcp_for)
+
+    # probabilities, rounded to their storage dtype
+    prob = sm.outputs[0].value
+    e = sm.out_expr[prob.name]
+    code, _ = elem_r(e) if _expr_varies(e, score_cols, vector) else scal_r(e)
+    L.append(f"  float pr[{NT}][4];")
+    L += elem_loop("pr", cast_code(code, k.prob_dtype)[0])
+    # O^T = V^T P^T, two 16-key tiles per MFMA
+    L.append("#pragma unroll")
+    L.append(f"  for (int dt = 0; dt < {D // 16}; ++dt) {{")
+    L.append("    mlc::float4v o = {0.0f, 0.0f, 0.0f, 0.0f};")
+    L.append(f"    const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 4;")
+    L.append("#pragma unroll")
+    L.append(f"    for (int m = 0; m < {NT // 2}; ++m) {{")
+    L.append("      const mlc::half4 lo = *reinterpret_cast<const mlc::half4*>(vrow + m * 32);")
+    L.append("      const mlc::half4 hi = *reinterpret_cast<const mlc::half4*>(vrow + m * 32 + 16);")
+    L.append("      const mlc::half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};")
+    L.append("      const mlc::half8 b = {(mlc::f16)pr[2 * m][0], (mlc::f16)pr[2 * m][1], "
+             "(mlc::f16)pr[2 * m][2], (mlc::f16)pr[2 * m][3], (mlc::f16)pr[2 * m + 1][0], "
+             "(mlc::f16)pr[2 * m + 1][1], (mlc::f16)pr[2 * m + 1][2], (mlc::f16)pr[2 * m + 1][3]};")
+    L.append("      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o, 0, 0, 0);")
+    L.append("    }")
+    ol = k.out.layout
+    L.append(f"    const mlc::half4 h = {{(mlc::f16)o[0], (mlc::f16)o[1], (mlc::f16)o[2], (mlc::f16)o[3]}};")
+    L.append(f"    *reinterpret_cast<mlc::half4*>(out0 + ({it}){ol.offset} + row * ({it}){D} "
+             f"+ ({it})(dt * 16 + g * 4)) = h;")
+    L.append("  }")
+    L.append("}")
+    spec = LaunchSpec("", BH * NQB, THREADS, lds_bytes,
+                      {"kind": "attention", "heads": BH, "queries": T, "keys": Tk, "head_dim": D,
+                       "queries_per_wg": QB})
+    return "\n".join(L), spec
+

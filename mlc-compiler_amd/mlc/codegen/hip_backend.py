@@ -42,7 +42,7 @@ import torch
 
 from ..config import Config
 from ..ir.scalar import Call, Cast, Const, Expr, Load, Ref, loads as expr_loads, refs as expr_refs
-from ..kernels import Bind, ExternKernel, PointwiseKernel, Reduce, ReductionKernel, Schedule
+from ..kernels import AttentionKernel, Bind, ExternKernel, PointwiseKernel, Reduce, ReductionKernel, Schedule
 from ..ir.graph import Value
 from .index import IndexMap, build_index
 from .reduction_schedule import plan_passes, scalar_binds, varies_by_column
@@ -1286,6 +1286,10 @@ def emit_kernel(k, cfg: Config) -> tuple[str, LaunchSpec] | None:
         return emit_reduction(k, cfg)
     if isinstance(k, ExternKernel):
         return emit_extern(k, cfg)
+    if isinstance(k, AttentionKernel):
+        from .hip_attention import emit_attention
+
+        return emit_attention(k, cfg)
     raise TypeError(f"no HIP emitter for {type(k).__name__}")
 
 

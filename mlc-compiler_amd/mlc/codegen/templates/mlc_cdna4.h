@@ -68,6 +68,12 @@ template <> __device__ __forceinline__ bool cvt<bool, int64_t>(int64_t x) { retu
 template <class S, class X> __device__ __forceinline__ void st(S* p, X x) { *p = cvt<S>(x); }
 
 // value rounded through a narrow float type, as a cast inside a kernel body
+// MFMA operand/accumulator fragments and a 16-byte bit copy of 8 halfs
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+struct alignas(16) f16x8 { f16 v[8]; };
+
 __device__ __forceinline__ float round_f16(float x) { return static_cast<float>(static_cast<f16>(x)); }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 

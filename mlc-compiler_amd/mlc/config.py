@@ -32,6 +32,9 @@ class Config:
     #: merge linear layers that read the same activation (BERT's q/k/v) into
     #: one GEMM over concatenated weights. A graph rewrite, off by default.
     merge_parallel_gemms: bool = False
+    #: one MFMA kernel per batch-head for bmm -> softmax -> bmm (scores and
+    #: probabilities never stored). A schedule change, off by default.
+    fused_attention: bool = False
 
     # codegen
     pointwise_block: int = 1024

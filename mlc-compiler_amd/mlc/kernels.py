@@ -147,6 +147,44 @@ class ReductionKernel(Kernel):
 
 
 @dataclass
+class AttentionKernel(Kernel):
+    """``out = steps(q @ kt) @ v`` per batch-head: a batched GEMM, the row
+    reduction that follows it and the batched GEMM that consumes that, as one
+    kernel (a schedule variant; the reference schedule keeps three). The
+    score and probability tensors are never stored, but their storage
+    roundings are kept: scores are rounded to ``score_dtype`` before the
+    reduction's steps and probabilities to ``prob_dtype`` before the second
+    GEMM, as the unfused schedule does.
+
+    ``inputs`` are q, kt, v, then the reduction's other inputs (index maps
+    over its ``row``/``col`` frame); ``softmax`` is the original reduction
+    kernel, whose slot ``score_slot`` read the scores."""
+
+    q: Value
+    kt: Value
+    v: Value
+    out: Value
+    softmax: "ReductionKernel"
+    score_slot: int
+    score_dtype: torch.dtype
+    prob_dtype: torch.dtype
+    inputs: list[KernelArg]
+    outputs: list[KernelArg]
+    nodes: list[Node] = field(default_factory=list)
+
+    def reads(self) -> list[Value]:
+        return [a.value for a in self.inputs]
+
+    def writes(self) -> list[Value]:
+        return [a.value for a in self.outputs]
+
+    def summary(self) -> str:
+        bh, t, d = self.q.shape
+        return (f"{self.name}: attention {bh}x[{t}x{d}]x[{self.kt.shape[2]}] "
+                f"{len(self.inputs)}in 1out [bmm, {_op_names(self.softmax.nodes)}, bmm]")
+
+
+@dataclass
 class ExternKernel(Kernel):
     """A library call (matmul, embedding, anything opaque)."""
 

@@ -25,6 +25,9 @@ from ..ir.capture import capture
 from . import native
 
 FAST = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True)
+ATTENTION = Config(fused_attention=True)
+ALL = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True,
+             fused_attention=True)
 
 #: every (workload, config) pair a committed caller compiles
 DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()),
@@ -33,7 +36,8 @@ DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()
            ("C4", Config(gemm_epilogue=True)), ("C4", Config(layout_selection=True)),
            ("C5", Config(layout_selection=True)),
            ("C4", Config(layout_selection=True, gemm_epilogue=True)),
-           ("C2", FAST), ("C4", FAST)]
+           ("C2", FAST), ("C4", FAST), ("C2", ATTENTION), ("C3", ATTENTION),
+           ("C4", ATTENTION), ("C2", ALL), ("C4", ALL)]
 
 
 def prebuild(items=None, verbose: bool = True) -> None:

@@ -37,7 +37,7 @@ from __future__ import annotations
 import torch
 
 from mlc.ir.scalar import Call, Cast, Const, Expr, Load, Ref
-from mlc.kernels import Bind, ExternKernel, PointwiseKernel, Reduce, ReductionKernel
+from mlc.kernels import AttentionKernel, Bind, ExternKernel, PointwiseKernel, Reduce, ReductionKernel
 
 TORCH_FN = {
     "neg": torch.neg, "abs": torch.abs, "reciprocal": torch.reciprocal,
@@ -244,11 +244,34 @@ def _as_two_pass(k: ReductionKernel) -> ReductionKernel:
     return twin
 
 
+def run_attention(k: AttentionKernel, buffers: dict[str, torch.Tensor]) -> None:
+    """The three kernels the fused one replaces, in order: ``bmm`` (fp32
+    products, rounded to the score dtype as the stored scores are), the
+    reduction kernel over a private score buffer, and ``bmm`` with the
+    values (reference: ``mlc/codegen/torch_backend.py:170-181`` for the
+    reduction; the GEMMs are the extern ``aten.bmm`` calls they replace)."""
+    q, kt, v = (_promote(x.layout.as_torch(buffers[x.buffer.name])) for x in (k.q, k.kt, k.v))
+    scores = torch.bmm(q, kt).to(k.score_dtype)
+    sm = k.softmax
+    score_buf = sm.inputs[k.score_slot].value.buffer
+    prob = sm.outputs[0].value
+    private = dict(buffers)
+    private[score_buf.name] = scores.reshape(-1)
+    private[prob.buffer.name] = torch.empty(prob.buffer.numel, dtype=prob.buffer.dtype,
+                                            device=scores.device)
+    run_reduction(sm, private, streamed=False)
+    p = _promote(private[prob.buffer.name].view(scores.shape))
+    out = k.out.layout.as_torch(buffers[k.out.buffer.name])
+    out.copy_(torch.bmm(p, v).to(out.dtype))
+
+
 def run_kernel(k, buffers: dict[str, torch.Tensor]) -> None:
     if isinstance(k, PointwiseKernel):
         run_pointwise(k, buffers)
     elif isinstance(k, ReductionKernel):
         run_reduction(k, buffers)
+    elif isinstance(k, AttentionKernel):
+        run_attention(k, buffers)
     else:
         raise TypeError(f"the oracle does not execute {type(k).__name__}")
 

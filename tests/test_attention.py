@@ -1,0 +1,177 @@
+"""Attention fusion (``Config.fused_attention``, an opt-in schedule change):
+what the pass fuses and refuses, the oracle's execution of the fused kernel
+against float64 attention, and the generated MFMA kernel's shape."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn as nn
+
+from mlc.api import build_pipeline
+from mlc.bench.models import build
+from mlc.bench.workloads import make
+from mlc.codegen.hip_backend import generate_module
+from mlc.config import Config
+from mlc.ir.capture import capture
+from mlc.kernels import AttentionKernel
+from mlc.passes.memory_planning import verify
+from mlc.runtime import native
+from oracle import compile_reference
+
+ATTN = Config(fused_attention=True, cuda_graphs=False)
+ALL = Config(fused_attention=True, merge_parallel_gemms=True, gemm_epilogue=True,
+             layout_selection=True, cuda_graphs=False)
+
+
+class Attention(nn.Module):
+    """softmax(q k^T / sqrt(d) + mask) v over [B, H, T, D] heads."""
+
+    def forward(self, q, k, v, mask):
+        scores = (q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1]) + mask
+        return scores.softmax(dim=-1) @ v
+
+
+class ScoresOut(Attention):
+    def forward(self, q, k, v, mask):
+        scores = (q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1]) + mask
+        return scores.softmax(dim=-1) @ v, scores
+
+
+def _inputs(b, h, t, tk, d, dtype=torch.float16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, h, t, d, generator=g).to(dtype)
+    k = torch.randn(b, h, tk, d, generator=g).to(dtype)
+    v = torch.randn(b, h, tk, d, generator=g).to(dtype)
+    mask = torch.where(torch.rand(b, 1, 1, tk, generator=g) < 0.2, -10000.0, 0.0).to(dtype)
+    return q, k, v, mask
+
+
+def _attention(sched):
+    return [k for k in sched.kernels if isinstance(k, AttentionKernel)]
+
+
+@pytest.mark.parametrize("key,cfg,n", [("C2", Config(fused_attention=True), 12),
+                                       ("C3", Config(fused_attention=True), 12),
+                                       ("C4", Config(fused_attention=True), 12),
+                                       ("C2", ALL, 12), ("C4", ALL, 12),
+                                       ("C5", Config(fused_attention=True), 0),
+                                       ("C1", Config(fused_attention=True), 0)])
+def test_workloads_fuse_every_layer(key, cfg, n):
+    model, args = make(key)
+    base = build_pipeline(capture(model, args), Config())
+    sched = build_pipeline(capture(model, args), cfg)
+    assert len(_attention(sched)) == n
+    if n:
+        # three kernels became one per layer
+        assert len(sched.kernels) <= len(base.kernels) - 2 * n
+        assert not verify(list(sched.plan.live_ranges.values()), sched.plan.offsets)
+        live = {v.buffer.name for k in sched.kernels for v in k.reads() + k.writes()}
+        for a in _attention(sched):
+            assert a.softmax.inputs[a.score_slot].value.buffer.name not in live
+            assert a.softmax.outputs[0].value.buffer.name not in live
+
+
+def test_refused_when_scores_escape_or_shapes_do_not_fit():
+    q, k, v, m = _inputs(1, 2, 32, 32, 64)
+    assert len(_attention(build_pipeline(capture(ScoresOut(), (q, k, v, m)), ATTN))) == 0
+    q, k, v, m = _inputs(1, 2, 160, 160, 64)  # longer than one workgroup holds
+    assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
+    q, k, v, m = _inputs(1, 2, 32, 32, 64, torch.float32)
+    assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
+    q, k, v, m = _inputs(1, 2, 32, 48, 64)  # keys not a multiple of 32
+    assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
+    q, k, v, m = _inputs(1, 2, 32, 32, 48)  # head size not a multiple of 32
+    assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 32, 32, 64), (1, 2, 80, 96, 32), (1, 1, 16, 128, 128)])
+def test_oracle_fused_attention_matches_float64(shape):
+    """The oracle's fused kernel (fp32 products rounded to fp16 scores, the
+    reduction's steps, fp16 probabilities, fp32 products) against attention
+    computed in float64 from the same fp16 inputs: within 2e-3 of the largest
+    output, and as close as the unfused schedule's oracle. A transposed
+    operand, a dropped scale or mask, or a wrong row mapping fails this."""
+    args = _inputs(*shape)
+    model = Attention()
+    sched = build_pipeline(capture(model, args), ATTN)
+    assert len(_attention(sched)) == 1
+    got = compile_reference(model, args, ATTN)(*args)
+    unfused = compile_reference(model, args, Config(cuda_graphs=False))(*args)
+    exact = model(*(a.double() for a in args))
+    scale = exact.abs().max().item()
+    err = (got.double() - exact).abs().max().item() / scale
+    err_unfused = (unfused.double() - exact).abs().max().item() / scale
+    assert err <= 2e-3
+    assert err <= max(2e-3, 2 * err_unfused)
+
+
+def test_oracle_fused_models_match_unfused():
+    for name in ("bert-small", "gpt-small"):
+        model, args = build(name, 2, 32, "cpu", torch.float16)
+        base = compile_reference(model, args, Config(cuda_graphs=False))(*args)
+        got = compile_reference(model, args, ATTN)(*args)
+        torch.testing.assert_close(got.float(), base.float(), rtol=1e-2, atol=5e-2)
+
+
+def test_generated_kernel_shape():
+    model, args = make("C2")
+    sched = build_pipeline(capture(model, args), ALL)
+    mod = generate_module(sched, ALL)
+    att = _attention(sched)
+    specs = {mod.launches[a.name].symbol for a in att}
+    assert len(specs) == 1, "every layer shares one attention function"
+    spec = mod.launches[att[0].name]
+    assert spec.meta["kind"] == "attention"
+    # 12 heads: two waves per workgroup, four workgroups per head
+    assert spec.block == 128 and spec.grid == 12 * 4
+    assert spec.lds_bytes <= 64 * 1024
+    body = mod.functions[spec.symbol]
+    assert body.count("__builtin_amdgcn_mfma_f32_16x16x32_f16") == 2
+    assert "__syncthreads();" in body and body.index("__syncthreads();") < body.index("return;")
+    # C2's merged-qkv views are unit-stride along the head dim: 128-bit LDS stores
+    assert body.count("*reinterpret_cast<mlc::f16x8*>(") == 2
+
+
+def test_attention_module_cross_compiles_for_gfx950(tmp_path, monkeypatch):
+    monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
+    for shape in ((1, 2, 80, 96, 32), (2, 3, 32, 32, 64)):
+        args = _inputs(*shape)
+        sched = build_pipeline(capture(Attention(), args), ATTN)
+        mod = generate_module(sched, ATTN)
+        _, obj = native.compile_code_object(mod.source)
+        assert obj.stat().st_size > 0
+
+
+def test_operand_producers_write_the_mfma_layouts():
+    """At batch > 1 BERT's K and V come from this compiler's own copy
+    kernels; the pass has them write K as [bh][key][d] and V as
+    [bh][d][key], so staging needs no transposing LDS stores."""
+    model, args = make("C4")
+    sched = build_pipeline(capture(model, args), ALL)
+    mod = generate_module(sched, ALL)
+    for a in _attention(sched):
+        assert a.kt.layout.strides == (128 * 64, 1, 64)
+        assert a.v.layout.strides == (128 * 64, 1, 128)
+        body = mod.functions[mod.launches[a.name].symbol]
+        assert body.count("*reinterpret_cast<mlc::f16x8*>(") == 3 and ".v[j]" not in body
+    assert not verify(list(sched.plan.live_ranges.values()), sched.plan.offsets)
+
+
+def test_relaid_out_operands_compute_the_same_values(monkeypatch):
+    """Moving K and V to other layouts changes where values are stored, not
+    what is computed: the oracle's result is bit-identical with and without
+    the relayout."""
+    import mlc.passes.attention as attention
+
+    model, args = build("bert-small", 2, 32, "cpu", torch.float16)
+    sched = build_pipeline(capture(model, args), ATTN)
+    assert all(a.v.layout.strides[1] == 1 for a in _attention(sched))
+    got = compile_reference(model, args, ATTN)(*args)
+    monkeypatch.setattr(attention, "_relayout_operands", lambda kernels, outputs: kernels)
+    sched = build_pipeline(capture(model, args), ATTN)
+    assert all(a.v.layout.strides[2] == 1 for a in _attention(sched))
+    want = compile_reference(model, args, ATTN)(*args)
+    assert torch.equal(got, want)

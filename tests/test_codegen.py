@@ -88,8 +88,8 @@ def test_access_modes():
 def test_reduction_geometry():
     g = reduction_geometry(4096, 768, 8)     # LayerNorm rows: 96 packs
     assert g["G"] * g["K"] * 8 == 768 and g["G"] <= 64 and g["K"] <= 8
-    g = reduction_geometry(49152, 128, 8)    # BERT softmax rows: 16 packs
-    assert g["G"] == 16 and g["K"] == 1 and g["block"] % 64 == 0
+    g = reduction_geometry(49152, 128, 8)    # BERT softmax rows: 16 packs, 2 per lane
+    assert g["G"] == 8 and g["K"] == 2 and g["block"] % 64 == 0
     g = reduction_geometry(10, 16384, 8)     # long rows span waves
     assert g["G"] > 64 and g["G"] * g["K"] * 8 >= 16384
 

@@ -183,6 +183,9 @@ STREAMED64 = Config(max_persistent_row=64)
 EPILOGUE = Config(gemm_epilogue=True)
 LAYOUT = Config(layout_selection=True)
 FAST = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True)
+ATTN = Config(fused_attention=True)
+ALL = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True,
+             fused_attention=True)
 
 
 @pytest.mark.parametrize("key,cfg,limit", [("C2", Config(), None), ("C3", Config(), None),
@@ -190,10 +193,14 @@ FAST = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=Tr
                                            ("C5", Config(), 16), ("C2", EPILOGUE, None),
                                            ("C3", EPILOGUE, None), ("C4", LAYOUT, None),
                                            ("C5", LAYOUT, 14), ("C2", FAST, None),
-                                           ("C4", FAST, None)],
+                                           ("C4", FAST, None), ("C2", ATTN, None),
+                                           ("C3", ATTN, None), ("C4", ATTN, None),
+                                           ("C2", ALL, None), ("C4", ALL, None)],
                          ids=["C2", "C3", "C4", "C2-streamed64", "C5-first-block",
                               "C2-gemm-epilogue", "C3-gemm-epilogue", "C4-layout",
-                              "C5-layout-first-block", "C2-all-variants", "C4-all-variants"])
+                              "C5-layout-first-block", "C2-all-variants", "C4-all-variants",
+                              "C2-attention", "C3-attention", "C4-attention",
+                              "C2-all-attention", "C4-all-attention"])
 def test_lockstep_every_kernel(key, cfg, limit):
     """Each generated kernel of the fp16 model, fed the oracle's own inputs:
     fp16 outputs within 2 ulp-scale (2e-3 relative to the largest magnitude),
@@ -230,9 +237,11 @@ def _truth_fp64(key):
 
 
 @pytest.mark.parametrize("key,cfg", [("C2", Config()), ("C3", Config()), ("C2", EPILOGUE),
-                                     ("C3", EPILOGUE), ("C2", FAST)],
+                                     ("C3", EPILOGUE), ("C2", FAST), ("C2", ATTN),
+                                     ("C3", ATTN), ("C2", ALL)],
                          ids=["C2", "C3", "C2-gemm-epilogue", "C3-gemm-epilogue",
-                              "C2-all-variants"])
+                              "C2-all-variants", "C2-attention", "C3-attention",
+                              "C2-all-attention"])
 def test_end_to_end_fp16(key, cfg):
     """Free-running HIP model (hipGraph replay) end to end in fp16.
 
@@ -373,3 +382,44 @@ def test_arena_is_one_slab_with_planned_offsets():
         t = compiled._resident.get(name)
         if t is not None:
             assert t.data_ptr() == base + off
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 32, 32, 64), (1, 2, 80, 96, 32), (1, 1, 16, 128, 128),
+                                   (3, 2, 128, 128, 64), (1, 4, 48, 64, 64)],
+                         ids=["b2h3-32x32-d64", "80x96-d32-partial-block", "16x128-d128",
+                              "b3h2-128x128-d64", "48x64-partial-block"])
+def test_fused_attention_shapes(shape):
+    """The MFMA attention kernel over shapes that exercise its edges: a
+    partial query block (80 queries, 64 per workgroup), more keys than
+    queries, head sizes 32 and 128, fewer than four waves. Against the
+    oracle's fused kernel on the same inputs and against float64 attention:
+    within 2e-3 of the largest output."""
+    from test_attention import Attention, _inputs
+
+    args = _inputs(*shape)
+    model = Attention()
+    want = compile_reference(model, args, Config(fused_attention=True, cuda_graphs=False))(*args)
+    exact = model(*(a.double() for a in args))
+    compiled = mlc.compile(model, tuple(a.cuda() for a in args), ATTN)
+    kinds = [s.meta["kind"] for s in compiled._module.launch_table.values()]
+    assert kinds.count("attention") == 1
+    got = compiled(*(a.cuda() for a in args))
+    torch.cuda.synchronize()
+    e_oracle, e_exact = rel_err(got, want), rel_err(got, exact)
+    print(shape, f"hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}")
+    assert e_oracle <= 2e-3 and e_exact <= 2e-3
+
+
+@pytest.mark.parametrize("key", ["C2", "C3"])
+def test_fused_attention_matches_reference_schedule(key):
+    """The fused-attention schedule computes the same function as the
+    reference schedule: outputs within 2e-3 of each other."""
+    gm, ga = make(key, "cuda")
+    ref = flat_outputs(mlc.compile(gm, ga, Config())(*ga))[0].clone()
+    compiled = mlc.compile(gm, ga, ATTN)
+    got = flat_outputs(compiled(*ga))[0]
+    torch.cuda.synchronize()
+    assert compiled.schedule.counts()["attention"] == 12
+    err = rel_err(got, ref)
+    print(key, "fused attention vs reference schedule: rel err", err)
+    assert err <= 2e-3
