@@ -21,7 +21,8 @@ One workgroup of ``W`` waves per (batch-head, block of ``16*W`` queries):
   MFMA pairs two 16-key tiles, so probabilities never leave registers; A is
   read from the transposed V tile with two ``ds_read_b64``. Lane ``l`` ends
   with four consecutive head-dim values of query ``l % 16``: one 8-byte
-  store each.
+  store each, at the output's index map over the flat ``[BH, T, D]`` index
+  (identity, or the permutation of a folded context copy).
 
 Numerics follow the unfused schedule: fp32 accumulation, scores and
 probabilities rounded to their storage dtypes before use, fp32 softmax.
@@ -34,8 +35,8 @@ from __future__ import annotations
 from ..kernels import AttentionKernel, Bind
 from .hip_backend import (_IDENTITY, _OP, WAVE, LaunchSpec, Renderer, _RowOffsets,
                           _expr_varies, _params, _reciprocal_divisors, _reciprocal_lines,
-                          _row_col_access, _scalar_division, cast_code,
-                          compute_type, index_type)
+                          _row_col_access, _scalar_division, axis_terms, cast_code,
+                          compute_type, index_type, join_offset, render_terms)
 from .reduction_schedule import varies_by_column
 
 #: waves per workgroup (each owns 16 queries): ``waves`` forces a count;
@@ -320,10 +321,13 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
              "(mlc::f16)pr[2 * m + 1][1], (mlc::f16)pr[2 * m + 1][2], (mlc::f16)pr[2 * m + 1][3]};")
     L.append("      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o, 0, 0, 0);")
     L.append("    }")
-    ol = k.out.layout
+    omap = k.outputs[0].index
+    parts = render_terms(axis_terms(omap, "idx"), BH * T * D, "f0", it)
+    if omap.base:
+        parts.append(f"({it}){omap.base}")
     L.append(f"    const mlc::half4 h = {{(mlc::f16)o[0], (mlc::f16)o[1], (mlc::f16)o[2], (mlc::f16)o[3]}};")
-    L.append(f"    *reinterpret_cast<mlc::half4*>(out0 + ({it}){ol.offset} + row * ({it}){D} "
-             f"+ ({it})(dt * 16 + g * 4)) = h;")
+    L.append(f"    const {it} f0 = row * ({it}){D} + ({it})(dt * 16 + g * 4);")
+    L.append(f"    *reinterpret_cast<mlc::half4*>(out0 + {join_offset(parts, it)}) = h;")
     L.append("  }")
     L.append("}")
     spec = LaunchSpec("", BH * NQB, THREADS, lds_bytes,

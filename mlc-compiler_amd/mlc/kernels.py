@@ -181,7 +181,7 @@ class AttentionKernel(Kernel):
     def summary(self) -> str:
         bh, t, d = self.q.shape
         return (f"{self.name}: attention {bh}x[{t}x{d}]x[{self.kt.shape[2]}] "
-                f"{len(self.inputs)}in 1out [bmm, {_op_names(self.softmax.nodes)}, bmm]")
+                f"{len(self.inputs)}in 1out [{_op_names(self.nodes)}]")
 
 
 @dataclass

@@ -19,7 +19,9 @@ multiple of 32 up to 128, fp16 operands (the MFMA the kernel is built on).
 When K or V is written by one of this compiler's pointwise kernels for the
 attention alone, that kernel is re-derived to write K as ``[bh][key][d]``
 and V as ``[bh][d][key]`` (the layouts the MFMA operands are read in), the
-same index-map composition layout selection uses.
+same index-map composition layout selection uses. A copy that only permutes
+the fused kernel's output (BERT's context re-layout) is folded into the
+kernel's stores.
 """
 
 from __future__ import annotations
@@ -34,7 +36,7 @@ from ..ir.graph import Value
 from ..ir.types import Layout
 from ..kernels import (AttentionKernel, ExternKernel, KernelArg, PointwiseKernel,
                        ReductionKernel, Schedule)
-from .layout import compose
+from .layout import is_pure_copy, compose
 
 MAX_SEQ = 128
 MAX_HEAD = 128
@@ -66,8 +68,60 @@ def fuse_attention(schedule: Schedule) -> int:
             replace[m] = att
             removed.update((i, j))
     new = [replace.get(i, k) for i, k in enumerate(kernels) if i not in removed]
-    schedule.kernels = _relayout_operands(new, graph_outputs)
+    new = _relayout_operands(new, graph_outputs)
+    schedule.kernels = _fold_output_copies(new, graph_outputs)
     return len(replace)
+
+
+def _output_copy(kernels, at: int, graph_outputs):
+    """(copy index, output arg) when the fused kernel's output is read only by
+    a copy that permutes it (BERT's context ``[BH, T, D] -> [B, T, H, D]``):
+    the output arg writes the copy's buffer directly, indexed by the fused
+    kernel's own flat output index. None when the permutation would break the
+    kernel's 8-byte stores of four consecutive head-dim values."""
+    k = kernels[at]
+    buf = k.out.buffer
+    readers = [i for i, x in enumerate(kernels) if any(v.buffer is buf for v in x.reads())]
+    if buf.name in graph_outputs or len(readers) != 1:
+        return None
+    j = readers[0]
+    c = kernels[j]
+    if not is_pure_copy(c) or c.inputs[0].value.buffer is not buf:
+        return None
+    view = c.inputs[0].value.layout
+    if view.offset != 0 or math.prod(view.shape) != buf.numel or c.numel != buf.numel:
+        return None
+    dest = Layout.contiguous(view.shape).strides
+    dims = sorted(((st, n, o) for st, n, o in zip(view.strides, view.shape, dest) if n != 1),
+                  key=lambda t: -t[0])
+    expect = 1
+    for st, n, _ in reversed(dims):  # a permutation of the contiguous output
+        if st != expect:
+            return None
+        expect *= n
+    shape = tuple(n for _, n, _ in dims)
+    imap = flat_index(shape, Layout(shape, tuple(o for _, _, o in dims), 0))
+    terms = imap.axes[0].terms if imap.axes else ()
+    inner = [t for t in terms if t[1] == 1]
+    if (imap.base % 4 or len(inner) != 1 or inner[0][2] != 1 or inner[0][0] % 4
+            or any(t[2] % 4 for t in terms if t is not inner[0])):
+        return None
+    return j, KernelArg(c.outputs[0].value, imap)
+
+
+def _fold_output_copies(kernels, graph_outputs):
+    out = list(kernels)
+    removed: set[int] = set()
+    for at, k in enumerate(out):
+        if not isinstance(k, AttentionKernel):
+            continue
+        found = _output_copy(out, at, graph_outputs)
+        if found is None:
+            continue
+        j, arg = found
+        out[at] = replace(k, out=arg.value, outputs=[arg], nodes=list(k.nodes) + list(out[j].nodes))
+        removed.add(j)
+    return [k for i, k in enumerate(out) if i not in removed]
 
 
 def _operand_producer(kernels, at: int, value, graph_outputs):

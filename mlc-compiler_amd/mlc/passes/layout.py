@@ -89,7 +89,7 @@ def compose(view: Layout, imap: IndexMap) -> Layout | None:
     return Layout(tuple(shape), tuple(deltas), base)
 
 
-def _pure_copy(k) -> bool:
+def is_pure_copy(k) -> bool:
     if not isinstance(k, PointwiseKernel) or len(k.inputs) != 1 or len(k.outputs) != 1:
         return False
     out = k.outputs[0]
@@ -119,7 +119,7 @@ def fold_relayout_copies(schedule: Schedule) -> int:
         copies = readers.get(out.buffer.name, [])
         if (not copies or out.buffer.name in graph_outputs or not p.outputs[0].index.is_identity()
                 or math.prod(p.space) != out.buffer.numel
-                or not all(_pure_copy(kernels[j]) for j in copies)):
+                or not all(is_pure_copy(kernels[j]) for j in copies)):
             continue
         fused = []
         for j in copies:

@@ -249,7 +249,9 @@ def run_attention(k: AttentionKernel, buffers: dict[str, torch.Tensor]) -> None:
     products, rounded to the score dtype as the stored scores are), the
     reduction kernel over a private score buffer, and ``bmm`` with the
     values (reference: ``mlc/codegen/torch_backend.py:170-181`` for the
-    reduction; the GEMMs are the extern ``aten.bmm`` calls they replace)."""
+    reduction; the GEMMs are the extern ``aten.bmm`` calls they replace).
+    The result is stored through the output's index map over its flat
+    ``[BH, T, D]`` index, which also covers a folded permuting copy."""
     q, kt, v = (_promote(x.layout.as_torch(buffers[x.buffer.name])) for x in (k.q, k.kt, k.v))
     scores = torch.bmm(q, kt).to(k.score_dtype)
     sm = k.softmax
@@ -261,8 +263,11 @@ def run_attention(k: AttentionKernel, buffers: dict[str, torch.Tensor]) -> None:
                                             device=scores.device)
     run_reduction(sm, private, streamed=False)
     p = _promote(private[prob.buffer.name].view(scores.shape))
-    out = k.out.layout.as_torch(buffers[k.out.buffer.name])
-    out.copy_(torch.bmm(p, v).to(out.dtype))
+    o = torch.bmm(p, v).reshape(-1)
+    arg = k.outputs[0]
+    dest = buffers[arg.value.buffer.name]
+    idx = torch.arange(o.numel(), device=o.device, dtype=torch.int64)
+    dest[_offsets(arg.index.render(), {"idx": idx}, idx)] = o.to(dest.dtype)
 
 
 def run_kernel(k, buffers: dict[str, torch.Tensor]) -> None:

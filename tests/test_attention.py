@@ -175,3 +175,24 @@ def test_relaid_out_operands_compute_the_same_values(monkeypatch):
     assert all(a.v.layout.strides[2] == 1 for a in _attention(sched))
     want = compile_reference(model, args, ATTN)(*args)
     assert torch.equal(got, want)
+
+
+def test_context_copy_folds_into_the_attention_stores():
+    """BERT's context copy ``[B*H, T, Dh] -> [B, T, H, Dh]`` only permutes the
+    attention output, so the fused kernel writes the copy's buffer through
+    the permutation and the copy disappears."""
+    for key, n_pointwise in (("C2", 15), ("C4", 51)):
+        model, args = make(key)
+        sched = build_pipeline(capture(model, args), ALL)
+        assert sched.counts()["pointwise"] == n_pointwise
+        for a in _attention(sched):
+            assert [n.op for n in a.nodes][-1] == "aten.clone.default"
+            assert a.outputs[0].index.render().endswith("* 768 + (idx % 64))")
+    # the oracle stores through the same permutation: compare with eager
+    model, args = build("bert-small", 2, 32, "cpu", torch.float16)
+    sched = build_pipeline(capture(model, args), ATTN)
+    assert all(not a.outputs[0].index.is_identity() for a in _attention(sched))
+    with torch.no_grad():
+        want = model(*args)
+    got = compile_reference(model, args, ATTN)(*args)
+    torch.testing.assert_close(got.float(), want.float(), rtol=1e-2, atol=5e-2)
