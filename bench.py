@@ -93,7 +93,7 @@ def _attention_row(compiled, iters: int) -> dict:
     gbs = rows[0][2] / (ms * 1e-3) / 1e9
     return {"symbol": rows[0][1], "launch_us": round(ms * 1e3, 3),
             "bytes_per_launch": rows[0][2], "achieved_gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": _measured_traffic(rows[0][1])}
 
 
 def _measured_traffic(symbol: str):

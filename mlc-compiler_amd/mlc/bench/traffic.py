@@ -9,9 +9,13 @@ It launches, ``--iters`` times each:
 1. a plain device copy of ``--copy-mib`` MiB (torch ``copy_``), whose true
    traffic is known (that many bytes read and written): the counters' scale
    factor is what they read for it divided by the true bytes;
-2. the dominant fused kernel of BERT-base fp16 b32 (config 4) -- the
-   generated function with the most device time per forward, fc1 bias +
-   GELU -- on the buffers of a compiled model, after one full forward.
+2. with ``--kernel gelu`` (the default), the dominant fused kernel of
+   BERT-base fp16 b32 (config 4) -- the generated function with the most
+   device time per forward, fc1 bias + GELU -- on the buffers of a compiled
+   model, after one full forward; with ``--kernel attention``, the fused
+   attention kernel of the same model compiled with every schedule variant
+   on (``merge_parallel_gemms``, ``gemm_epilogue``, ``layout_selection``,
+   ``fused_attention``).
 
 It prints each kernel's symbol and algorithmic bytes per launch so the
 counter CSV can be matched to them.
@@ -33,6 +37,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--iters", type=int, default=5)
     ap.add_argument("--copy-mib", type=int, default=1024)
+    ap.add_argument("--kernel", choices=("gelu", "attention"), default="gelu")
     opts = ap.parse_args()
 
     import torch
@@ -41,7 +46,7 @@ def main() -> int:
     from mlc.bench.roofline import algorithmic_bytes
     from mlc.bench.workloads import make
     from mlc.config import Config
-    from mlc.kernels import PointwiseKernel
+    from mlc.kernels import AttentionKernel, PointwiseKernel
 
     torch.cuda.set_device(0)
     n = opts.copy_mib * (1 << 20) // 2
@@ -54,18 +59,29 @@ def main() -> int:
     print(f"copy: {2 * n} bytes read + {2 * n} bytes written per launch", flush=True)
 
     model, inputs = make("C4", "cuda")
-    compiled = mlc.compile(model, inputs, Config(cuda_graphs=False))
+    if opts.kernel == "gelu":
+        cfg = Config(cuda_graphs=False)
+
+        def wanted(k):
+            return (isinstance(k, PointwiseKernel)
+                    and any(nd.op == "aten.erf.default" for nd in k.nodes))
+    else:
+        cfg = Config(cuda_graphs=False, merge_parallel_gemms=True, gemm_epilogue=True,
+                     layout_selection=True, fused_attention=True)
+
+        def wanted(k):
+            return isinstance(k, AttentionKernel)
+    compiled = mlc.compile(model, inputs, cfg)
     compiled(*inputs)
     torch.cuda.synchronize()
     rt = compiled._module
-    gelu = [(k, p) for k, (kind, p) in zip(compiled.schedule.kernels, compiled._plan)
-            if kind == "kernel" and isinstance(k, PointwiseKernel)
-            and any(nd.op == "aten.erf.default" for nd in k.nodes)]
-    k, bound = gelu[-1]
+    found = [(k, p) for k, (kind, p) in zip(compiled.schedule.kernels, compiled._plan)
+             if kind == "kernel" and wanted(k)]
+    k, bound = found[-1]
     for _ in range(opts.iters):
         rt.run_bound(bound)
     torch.cuda.synchronize()
-    print(f"dominant: {rt.launch_table[k.name].symbol} {k.summary()} "
+    print(f"{opts.kernel}: {rt.launch_table[k.name].symbol} {k.summary()} "
           f"algorithmic_bytes={algorithmic_bytes(k)}", flush=True)
     return 0
 
