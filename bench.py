@@ -9,9 +9,14 @@ in HBM. ``value`` is ms per forward at b1; b32 (config 4)
 is timed the same way and reported beside it. The roofline object covers the
 dominant fused kernel at b32 (the function moving the most algorithmic bytes
 per forward), timed with hipEvents on its launch stream, with its
-counter-measured traffic from the committed PMC summary in ``profiles/``; ``fused_b32`` aggregates every fused kernel.
-The CPU baseline is the oracle (the kernel IR executed with torch on the
-host) on a bounded number of b1 forwards. Prints one JSON line.
+counter-measured traffic from the committed PMC summary in ``profiles/``;
+``fused_b32`` aggregates every fused kernel. Beside each kernel figure,
+``copy_ceiling`` times a plain packed copy kernel of the same algorithmic
+bytes the same way: the practical ceiling once each launch's fixed cost is
+counted.
+``schedule_variants`` times the opt-in schedule changes (never the headline
+value). The CPU baseline is the oracle (the kernel IR executed with torch on
+the host) on a bounded number of b1 forwards. Prints one JSON line.
 """
 
 from __future__ import annotations
@@ -59,6 +64,29 @@ def _time_replays(compiled, inputs, steps: int, warmup: int):
     }
 
 
+_CEILING = None
+
+
+def _copy_period_us(nbytes: int, iters: int) -> float:
+    """Back-to-back launch period of a plain packed copy moving ``nbytes``
+    (half read, half written), timed like the kernel table
+    (``mlc.bench.copy_ceiling``)."""
+    import torch
+
+    from mlc.bench.copy_ceiling import CopyCeiling
+
+    global _CEILING
+    if _CEILING is None:
+        _CEILING = CopyCeiling(torch.cuda.current_device())
+    return _CEILING.period_us(nbytes, iters, torch.cuda.current_stream().cuda_stream)
+
+
+def _copy_ceiling(nbytes: int, kernel_us: float, iters: int) -> dict:
+    copy_us = _copy_period_us(nbytes, iters)
+    return {"copy_us": round(copy_us, 3), "copy_gbs": round(nbytes / copy_us / 1e3, 1),
+            "kernel_vs_copy": round(copy_us / kernel_us, 4)}
+
+
 def _kernel_table(compiled, iters: int):
     """(kernel, symbol, algorithmic bytes, avg ms) of every generated kernel,
     each launched ``iters`` times back to back and timed with hipEvents on
@@ -93,7 +121,8 @@ def _attention_row(compiled, iters: int) -> dict:
     gbs = rows[0][2] / (ms * 1e-3) / 1e9
     return {"symbol": rows[0][1], "launch_us": round(ms * 1e3, 3),
             "bytes_per_launch": rows[0][2], "achieved_gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": _measured_traffic(rows[0][1])}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": _measured_traffic(rows[0][1]),
+            "copy_ceiling": _copy_ceiling(rows[0][2], ms * 1e3, iters)}
 
 
 def _measured_traffic(symbol: str):
@@ -220,6 +249,9 @@ def main() -> int:
     fused_bytes = sum(r[2] for r in rows)
     fused_ms = sum(r[3] for r in rows)
     fused_gbs = fused_bytes / (fused_ms * 1e-3) / 1e9
+    # the same launches as plain copies of each kernel's bytes
+    copy_of = {b: _copy_period_us(b, opts.kernel_iters) for b in {r[2] for r in rows}}
+    copy_ms = sum(copy_of[r[2]] for r in rows) / 1e3
 
     line = {
         "metric": METRIC,
@@ -254,6 +286,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _measured_traffic(dom_sym),
+            "copy_ceiling": _copy_ceiling(dom["bytes"], launch_ms * 1e3, opts.kernel_iters),
         },
         "fused_b32": {
             "kernels": len(rows),
@@ -261,6 +294,8 @@ def main() -> int:
             "ms": round(fused_ms, 4),
             "achieved": round(fused_gbs, 1),
             "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
+            "copy_ceiling_ms": round(copy_ms, 4),
+            "kernels_vs_copy": round(copy_ms / fused_ms, 4),
         },
         "cpu_baseline": None,
     }

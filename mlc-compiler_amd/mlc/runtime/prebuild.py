@@ -41,6 +41,9 @@ DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()
 
 
 def prebuild(items=None, verbose: bool = True) -> None:
+    from ..bench.copy_ceiling import SOURCE as COPY_CEILING
+
+    native.compile_code_object(COPY_CEILING)
     for key, cfg in (items or DEFAULT):
         t0 = time.time()
         model, args = make(key, "cpu")

@@ -184,3 +184,13 @@ def test_module_cross_compiles_for_gfx950(name, cfg, tmp_path, monkeypatch):
     # cached: a second request does not recompile
     mtime = obj.stat().st_mtime_ns
     assert native.compile_code_object(mod.source)[1].stat().st_mtime_ns == mtime
+
+
+def test_copy_ceiling_kernel_cross_compiles(tmp_path, monkeypatch):
+    """The plain packed copy the bench compares kernels with builds for gfx950
+    with the same flags and header as the generated modules."""
+    from mlc.bench.copy_ceiling import SOURCE
+
+    monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
+    _, obj = native.compile_code_object(SOURCE)
+    assert obj.stat().st_size > 0
