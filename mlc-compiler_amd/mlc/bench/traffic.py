@@ -15,7 +15,9 @@ It launches, ``--iters`` times each:
    model, after one full forward; with ``--kernel attention``, the fused
    attention kernel of the same model compiled with every schedule variant
    on (``merge_parallel_gemms``, ``gemm_epilogue``, ``layout_selection``,
-   ``fused_attention``).
+   ``fused_attention``); with ``--kernel all``, every generated kernel of
+   the reference schedule at config 4 (for per-kernel counters such as
+   ``SQ_INSTS_VALU``).
 
 It prints each kernel's symbol and algorithmic bytes per launch so the
 counter CSV can be matched to them.
@@ -37,7 +39,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--iters", type=int, default=5)
     ap.add_argument("--copy-mib", type=int, default=1024)
-    ap.add_argument("--kernel", choices=("gelu", "attention"), default="gelu")
+    ap.add_argument("--kernel", choices=("gelu", "attention", "all"), default="gelu")
     opts = ap.parse_args()
 
     import torch
@@ -65,24 +67,31 @@ def main() -> int:
         def wanted(k):
             return (isinstance(k, PointwiseKernel)
                     and any(nd.op == "aten.erf.default" for nd in k.nodes))
-    else:
+    elif opts.kernel == "attention":
         cfg = Config(cuda_graphs=False, merge_parallel_gemms=True, gemm_epilogue=True,
                      layout_selection=True, fused_attention=True)
 
         def wanted(k):
             return isinstance(k, AttentionKernel)
+    else:
+        cfg = Config(cuda_graphs=False)
+
+        def wanted(k):
+            return True
     compiled = mlc.compile(model, inputs, cfg)
     compiled(*inputs)
     torch.cuda.synchronize()
     rt = compiled._module
     found = [(k, p) for k, (kind, p) in zip(compiled.schedule.kernels, compiled._plan)
              if kind == "kernel" and wanted(k)]
-    k, bound = found[-1]
-    for _ in range(opts.iters):
-        rt.run_bound(bound)
-    torch.cuda.synchronize()
-    print(f"{opts.kernel}: {rt.launch_table[k.name].symbol} {k.summary()} "
-          f"algorithmic_bytes={algorithmic_bytes(k)}", flush=True)
+    if opts.kernel != "all":
+        found = found[-1:]
+    for k, bound in found:
+        for _ in range(opts.iters):
+            rt.run_bound(bound)
+        torch.cuda.synchronize()
+        print(f"{opts.kernel}: {rt.launch_table[k.name].symbol} {k.summary()} "
+              f"algorithmic_bytes={algorithmic_bytes(k)}", flush=True)
     return 0
 
 
