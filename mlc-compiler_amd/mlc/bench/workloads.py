@@ -6,6 +6,8 @@ C2  BERT-base fp16 b1 s128.
 C3  GPT-2 small fp16 b1 s128.
 C4  BERT-base fp16 b32 s128.
 C5  GPT-2 small fp16 b32 s512.
+C2-fp32  BERT-base fp32 b1 s128 (compiled by the reference's GPU check too;
+    a parity case for the fp32 bar, not a benchmark line).
 
 BERT/GPT weights: Linear and Embedding ~ N(0, 0.02), biases 0, LayerNorm
 (1, 0); inputs are ``input_ids ~ U[0, vocab)`` (and an all-ones attention
@@ -38,6 +40,7 @@ WORKLOADS = {
     "C3": Workload("C3", "gpt2-small", 1, 128, torch.float16, "GPT-2 small fp16 b1 s128"),
     "C4": Workload("C4", "bert-base", 32, 128, torch.float16, "BERT-base fp16 b32 s128"),
     "C5": Workload("C5", "gpt2-small", 32, 512, torch.float16, "GPT-2 small fp16 b32 s512"),
+    "C2-fp32": Workload("C2-fp32", "bert-base", 1, 128, torch.float32, "BERT-base fp32 b1 s128"),
 }
 
 

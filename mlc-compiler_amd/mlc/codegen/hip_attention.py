@@ -27,7 +27,8 @@ One workgroup of ``W`` waves per (batch-head, block of ``16*W`` queries):
 Numerics follow the unfused schedule: fp32 accumulation, scores and
 probabilities rounded to their storage dtypes before use, fp32 softmax.
 Summation orders differ from the library GEMMs and from the standalone
-reduction kernel, so results agree to rounding, not bit for bit.
+reduction kernel, and the softmax's exp and division take fast forms
+(``FAST_SOFTMAX_MATH``), so results agree to fp16 rounding, not bit for bit.
 """
 
 from __future__ import annotations
@@ -38,6 +39,12 @@ from .hip_backend import (_IDENTITY, _OP, WAVE, LaunchSpec, Renderer, _RowOffset
                           _row_col_access, _scalar_division, axis_terms, cast_code,
                           compute_type, index_type, join_offset, render_terms)
 from .reduction_schedule import varies_by_column
+
+#: the softmax's exp and its division by the row sum in fast forms
+#: (``mlc::exp_fast`` and a multiply by the row reciprocal). Both are used only
+#: here, where every probability is rounded to fp16 before it is used: their
+#: errors (about 1e-6 and 1.5 fp32 ulp) are far below that rounding.
+FAST_SOFTMAX_MATH = True
 
 #: waves per workgroup (each owns 16 queries): ``waves`` forces a count;
 #: otherwise the largest of ``choices`` that still gives ``min_workgroups``
@@ -56,6 +63,15 @@ def attention_waves(heads: int, queries: int) -> int:
         if heads * -(-queries // (16 * w)) >= ATTENTION_TUNING["min_workgroups"]:
             return w
     return choices[-1]
+
+
+class _FastExpRenderer(Renderer):
+    def call(self, e):
+        if e.fn == "exp":
+            code, t = self(e.args[0])
+            if t == "float":
+                return f"mlc::exp_fast({code})", "float"
+        return super().call(e)
 
 
 def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc: int, pr: int,
@@ -251,8 +267,9 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
             raise AssertionError("vector temp read in a row-scalar expression")
         return name, temp_types[name]
 
-    elem_r = Renderer(ref_elem, temp_elem)
-    scal_r = Renderer(ref_scalar, temp_scalar)
+    R_ = _FastExpRenderer if FAST_SOFTMAX_MATH else Renderer
+    elem_r = R_(ref_elem, temp_elem)
+    scal_r = R_(ref_scalar, temp_scalar)
     rcp_for = _reciprocal_divisors(sm, vector)
     score_cols = set(col_slots) | {k.score_slot}
 
@@ -270,7 +287,9 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
                 if sd is not None and t == "float":
                     num, d = elem_r(sd[0])[0], sd[1]
                     L.append(f"  if (__all(ok_{d})) {{")
-                    L += elem_loop(st.name, f"mlc::div_rcp({num}, {d}, rcp_{d})")
+                    fast = (f"({num} * rcp_{d})" if FAST_SOFTMAX_MATH
+                            else f"mlc::div_rcp({num}, {d}, rcp_{d})")
+                    L += elem_loop(st.name, fast)
                     L.append("  } else {")
                     L += elem_loop(st.name, code)
                     L.append("  }")

@@ -21,6 +21,7 @@ output -- is still hot in cache).
 
 from __future__ import annotations
 
+import functools
 import math
 
 import numpy as np
@@ -69,9 +70,11 @@ def _sample(shape):
                            np.array(corners, dtype=np.int64)])
 
 
+@functools.lru_cache(maxsize=4096)
 def compose(view: Layout, imap: IndexMap) -> Layout | None:
     """The layout, over ``view``'s shape, of ``imap`` read at the offsets
-    ``view`` addresses -- or None when that read is not affine."""
+    ``view`` addresses -- or None when that read is not affine. Memoised:
+    every transformer layer asks the same question."""
     shape = view.shape
     base = int(_eval(imap, np.array([view.offset], dtype=np.int64))[0])
     deltas = []

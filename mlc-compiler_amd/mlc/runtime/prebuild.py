@@ -31,7 +31,7 @@ ALL = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=Tru
 
 #: every (workload, config) pair a committed caller compiles
 DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()),
-           ("C5", Config()), ("C2", Config(max_persistent_row=64)),
+           ("C5", Config()), ("C2-fp32", Config()), ("C2", Config(max_persistent_row=64)),
            ("C2", Config(gemm_epilogue=True)), ("C3", Config(gemm_epilogue=True)),
            ("C4", Config(gemm_epilogue=True)), ("C4", Config(layout_selection=True)),
            ("C5", Config(layout_selection=True)),

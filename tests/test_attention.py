@@ -12,7 +12,6 @@ import torch.nn as nn
 
 from mlc.api import build_pipeline
 from mlc.bench.models import build
-from mlc.bench.workloads import make
 from mlc.codegen.hip_backend import generate_module
 from mlc.config import Config
 from mlc.ir.capture import capture
@@ -20,6 +19,7 @@ from mlc.kernels import AttentionKernel
 from mlc.passes.memory_planning import verify
 from mlc.runtime import native
 from oracle import compile_reference
+from workload_cache import graph_of
 
 ATTN = Config(fused_attention=True, cuda_graphs=False)
 ALL = Config(fused_attention=True, merge_parallel_gemms=True, gemm_epilogue=True,
@@ -60,9 +60,8 @@ def _attention(sched):
                                        ("C5", Config(fused_attention=True), 0),
                                        ("C1", Config(fused_attention=True), 0)])
 def test_workloads_fuse_every_layer(key, cfg, n):
-    model, args = make(key)
-    base = build_pipeline(capture(model, args), Config())
-    sched = build_pipeline(capture(model, args), cfg)
+    base = build_pipeline(graph_of(key), Config())
+    sched = build_pipeline(graph_of(key), cfg)
     assert len(_attention(sched)) == n
     if n:
         # three kernels became one per layer
@@ -117,8 +116,7 @@ def test_oracle_fused_models_match_unfused():
 
 
 def test_generated_kernel_shape():
-    model, args = make("C2")
-    sched = build_pipeline(capture(model, args), ALL)
+    sched = build_pipeline(graph_of("C2"), ALL)
     mod = generate_module(sched, ALL)
     att = _attention(sched)
     specs = {mod.launches[a.name].symbol for a in att}
@@ -149,8 +147,7 @@ def test_operand_producers_write_the_mfma_layouts():
     """At batch > 1 BERT's K and V come from this compiler's own copy
     kernels; the pass has them write K as [bh][key][d] and V as
     [bh][d][key], so staging needs no transposing LDS stores."""
-    model, args = make("C4")
-    sched = build_pipeline(capture(model, args), ALL)
+    sched = build_pipeline(graph_of("C4"), ALL)
     mod = generate_module(sched, ALL)
     for a in _attention(sched):
         assert a.kt.layout.strides == (128 * 64, 1, 64)
@@ -182,8 +179,7 @@ def test_context_copy_folds_into_the_attention_stores():
     attention output, so the fused kernel writes the copy's buffer through
     the permutation and the copy disappears."""
     for key, n_pointwise in (("C2", 15), ("C4", 51)):
-        model, args = make(key)
-        sched = build_pipeline(capture(model, args), ALL)
+        sched = build_pipeline(graph_of(key), ALL)
         assert sched.counts()["pointwise"] == n_pointwise
         for a in _attention(sched):
             assert [n.op for n in a.nodes][-1] == "aten.clone.default"

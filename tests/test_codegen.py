@@ -12,7 +12,6 @@ import pytest
 import torch
 
 from mlc.api import build_pipeline
-from mlc.bench.workloads import make
 from mlc.codegen.hip_backend import (classify_access, emit_kernel, float_literal,
                                      generate_module, reduction_geometry)
 from mlc.codegen.index import build_index, flat_index
@@ -22,6 +21,7 @@ from mlc.ir.types import Layout
 from mlc.kernels import ExternKernel, PointwiseKernel, ReductionKernel
 from mlc.runtime import native
 from models import all_models
+from workload_cache import graph_of
 
 FULL = Config(cuda_graphs=False)
 STREAMED = Config(cuda_graphs=False, max_persistent_row=4)
@@ -128,8 +128,7 @@ def test_generation_is_deterministic():
 
 
 def test_layers_share_kernel_code():
-    model, args = make("C2")
-    sched = build_pipeline(capture(model, args), Config())
+    sched = build_pipeline(graph_of("C2"), Config())
     mod = generate_module(sched, Config())
     generated = [k for k in sched.kernels if not isinstance(k, ExternKernel)]
     assert len(generated) == 100
@@ -137,8 +136,7 @@ def test_layers_share_kernel_code():
 
 
 def test_fp16_contiguous_operands_move_in_128bit_packs():
-    model, args = make("C4")
-    sched = build_pipeline(capture(model, args), Config())
+    sched = build_pipeline(graph_of("C4"), Config())
     mod = generate_module(sched, Config())
     gelu = next(k for k in sched.kernels if isinstance(k, PointwiseKernel)
                 and any(n.op == "aten.erf.default" for n in k.nodes))
@@ -151,8 +149,7 @@ def test_fp16_contiguous_operands_move_in_128bit_packs():
 
 
 def test_embedding_runs_as_a_native_template():
-    model, args = make("C2")
-    sched = build_pipeline(capture(model, args), Config())
+    sched = build_pipeline(graph_of("C2"), Config())
     mod = generate_module(sched, Config())
     embs = [k for k in sched.kernels if isinstance(k, ExternKernel)
             and k.node.op == "aten.embedding.default"]

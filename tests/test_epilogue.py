@@ -9,13 +9,13 @@ import torch.nn as nn
 
 from mlc.api import build_pipeline
 from mlc.bench.models import build
-from mlc.bench.workloads import make
 from mlc.config import Config
 from mlc.ir.capture import capture
 from mlc.kernels import ExternKernel, PointwiseKernel
 from mlc.passes.memory_planning import verify
 from models import all_models
 from oracle import compile_reference
+from workload_cache import graph_of
 
 EPI = Config(gemm_epilogue=True, cuda_graphs=False)
 
@@ -26,9 +26,8 @@ def _addmms(sched):
 
 
 def test_bert_qkv_bias_adds_fold_into_the_gemm():
-    model, args = make("C2")
-    base = build_pipeline(capture(model, args), Config())
-    sched = build_pipeline(capture(model, args), Config(gemm_epilogue=True))
+    base = build_pipeline(graph_of("C2"), Config())
+    sched = build_pipeline(graph_of("C2"), Config(gemm_epilogue=True))
     assert len(_addmms(sched)) == 36
     assert sched.counts() == {"extern": 100, "pointwise": 27, "reduction": 37}
     assert base.counts()["pointwise"] - sched.counts()["pointwise"] == 36
@@ -44,15 +43,13 @@ def test_bert_qkv_bias_adds_fold_into_the_gemm():
 
 
 def test_gpt2_fused_qkv_bias_folds():
-    model, args = make("C3")
-    sched = build_pipeline(capture(model, args), Config(gemm_epilogue=True))
+    sched = build_pipeline(graph_of("C3"), Config(gemm_epilogue=True))
     assert len(_addmms(sched)) == 12
     assert all(k.outputs[0].shape == (128, 2304) for k in _addmms(sched))
 
 
 def test_default_config_keeps_the_reference_schedule():
-    model, args = make("C2")
-    sched = build_pipeline(capture(model, args), Config())
+    sched = build_pipeline(graph_of("C2"), Config())
     assert not _addmms(sched)
 
 

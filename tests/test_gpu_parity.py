@@ -228,6 +228,30 @@ def test_lockstep_every_kernel(key, cfg, limit):
     print(key, "worst per-kernel rel err", max(worst.values()))
 
 
+def test_bert_base_fp32_end_to_end():
+    """BERT-base b1 s128 in fp32, which the reference's own GPU check also
+    compiles: the replayed hipGraph against the oracle chain (CPU oracle
+    kernels sharing the GPU's extern results, so library GEMM differences do
+    not count) at the fp32 bar, rel err <= 1e-5, and against eager fp32."""
+    model, args = make("C2-fp32", "cpu")
+    graph = capture(model, args)
+    cfg = Config()
+    schedule = build_pipeline(graph, cfg)
+    rt = HipRuntime(schedule, cfg, torch.device("cuda:0"))
+    ref = lockstep(schedule, graph, _params_by_buffer(graph), args, rt, None)
+    gm, ga = model.to("cuda"), tuple(a.to("cuda") for a in args)
+    got = flat_outputs(mlc.compile(gm, ga, cfg)(*ga))
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        eager = flat_outputs(gm(*ga))
+    for g, v, e in zip(got, graph.outputs, eager):
+        want = v.layout.as_torch(ref[v.buffer.name])
+        err, err_eager = rel_err(g, want), rel_err(g, e)
+        print(f"bert-base fp32 {v.name}: hip-vs-oracle {err:.2e}, hip-vs-eager {err_eager:.2e}")
+        assert err <= 1e-5
+        assert err_eager <= 1e-4
+
+
 def _truth_fp64(key):
     model, args = make(key, "cpu")
     model = model.double()
@@ -413,13 +437,22 @@ def test_fused_attention_shapes(shape):
 @pytest.mark.parametrize("key", ["C2", "C3"])
 def test_fused_attention_matches_reference_schedule(key):
     """The fused-attention schedule computes the same function as the
-    reference schedule: outputs within 2e-3 of each other."""
+    reference schedule. Two fp16 implementations of a 12-layer model drift
+    apart by rounding flips (eager PyTorch and the reference schedule differ
+    by about 3e-3 on BERT's pooled output), so, as in the end-to-end test, the
+    2e-3 bar is applied against the exact (float64) result, and the distance
+    to the reference schedule may be no larger than eager PyTorch's."""
     gm, ga = make(key, "cuda")
     ref = flat_outputs(mlc.compile(gm, ga, Config())(*ga))[0].clone()
     compiled = mlc.compile(gm, ga, ATTN)
     got = flat_outputs(compiled(*ga))[0]
     torch.cuda.synchronize()
+    with torch.no_grad():
+        eager = flat_outputs(gm(*ga))[0]
     assert compiled.schedule.counts()["attention"] == 12
-    err = rel_err(got, ref)
-    print(key, "fused attention vs reference schedule: rel err", err)
-    assert err <= 2e-3
+    truth = _truth_fp64(key)[0]
+    err, err_truth, err_eager = rel_err(got, ref), rel_err(got, truth), rel_err(eager, ref)
+    print(f"{key} fused attention: vs reference schedule {err:.2e} (eager vs reference "
+          f"schedule {err_eager:.2e}), vs float64 {err_truth:.2e}")
+    assert err_truth <= 2e-3
+    assert err <= max(2e-3, err_eager)

@@ -10,19 +10,18 @@ import torch.nn as nn
 
 from mlc.api import build_pipeline
 from mlc.bench.models import build
-from mlc.bench.workloads import make
 from mlc.config import Config
 from mlc.ir.capture import capture
 from mlc.kernels import ExternKernel
 from mlc.passes.horizontal import merge_parallel_gemms
 from oracle import compile_reference
+from workload_cache import graph_of
 
 MERGE = Config(merge_parallel_gemms=True, cuda_graphs=False)
 
 
 def test_bert_qkv_become_one_gemm_per_layer():
-    model, args = make("C2")
-    g = capture(model, args)
+    g = graph_of("C2")
     n_params = len(g.params)
     assert merge_parallel_gemms(g) == 24
     g.topo_check()
@@ -35,15 +34,13 @@ def test_bert_qkv_become_one_gemm_per_layer():
 
 
 def test_with_the_epilogue_the_merged_bias_folds_too():
-    model, args = make("C2")
-    sched = build_pipeline(capture(model, args), Config(merge_parallel_gemms=True,
+    sched = build_pipeline(graph_of("C2"), Config(merge_parallel_gemms=True,
                                                         gemm_epilogue=True))
     assert sched.counts() == {"extern": 76, "pointwise": 27, "reduction": 37}
 
 
 def test_gpt2_is_already_merged():
-    model, args = make("C3")
-    assert merge_parallel_gemms(capture(model, args)) == 0
+    assert merge_parallel_gemms(graph_of("C3")) == 0
 
 
 def test_merged_model_matches_eager():

@@ -8,16 +8,15 @@ import torch
 
 from mlc.api import build_pipeline
 from mlc.bench.models import build
-from mlc.bench.workloads import make
 from mlc.codegen.hip_backend import generate_module
 from mlc.codegen.index import flat_index
 from mlc.config import Config
-from mlc.ir.capture import capture
 from mlc.ir.types import Layout
 from mlc.kernels import PointwiseKernel
 from mlc.passes.layout import compose
 from mlc.passes.memory_planning import verify
 from oracle import compile_reference
+from workload_cache import graph_of
 
 LAYOUT = Config(layout_selection=True)
 
@@ -49,9 +48,8 @@ def _pointwise(s):
 
 
 def test_bert_b32_copies_merge_into_bias_adds():
-    model, args = make("C4")
-    base = build_pipeline(capture(model, args), Config())
-    sched = build_pipeline(capture(model, args), LAYOUT)
+    base = build_pipeline(graph_of("C4"), Config())
+    sched = build_pipeline(graph_of("C4"), LAYOUT)
     assert sched.counts() == {"extern": 100, "pointwise": 63, "reduction": 37}
     merged = [k for k in _pointwise(sched)
               if [n.op for n in k.nodes] == ["aten.add.Tensor", "aten.clone.default"]]
@@ -64,15 +62,13 @@ def test_bert_b32_copies_merge_into_bias_adds():
 
 
 def test_gpt2_b32_fused_qkv_add_splits_into_three_merged_kernels():
-    model, args = make("C5")
-    sched = build_pipeline(capture(model, args), LAYOUT)
+    sched = build_pipeline(graph_of("C5"), LAYOUT)
     assert sched.counts() == {"extern": 75, "reduction": 37, "pointwise": 60}
-    assert sched.arena_bytes < build_pipeline(capture(model, args), Config()).arena_bytes
+    assert sched.arena_bytes < build_pipeline(graph_of("C5"), Config()).arena_bytes
 
 
 def test_batch_one_has_nothing_to_merge():
-    model, args = make("C2")
-    assert build_pipeline(capture(model, args), LAYOUT).counts()["pointwise"] == 63
+    assert build_pipeline(graph_of("C2"), LAYOUT).counts()["pointwise"] == 63
 
 
 def test_merged_schedule_is_bit_identical_to_the_reference_schedule():

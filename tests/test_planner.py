@@ -10,13 +10,13 @@ import pytest
 import torch
 
 from mlc.api import build_pipeline
-from mlc.bench.workloads import make
 from mlc.config import Config
 from mlc.ir.capture import capture
 from mlc.ir.types import Buffer, Layout
 from mlc.passes.memory_planning import ALIGNMENT, LiveRange, pack, peak_live_bytes, verify
 from models import all_models
 from oracle import compile_reference
+from workload_cache import graph_of
 
 PLANNED = Config(reduction_fusion=False, cuda_graphs=False)
 UNPLANNED = Config(reduction_fusion=False, cuda_graphs=False, memory_planning=False)
@@ -98,8 +98,7 @@ def _bert_closed_form(B, T, e, D=768, FF=3072):
 
 @pytest.mark.parametrize("key,B,e", [("C2", 1, 2)])
 def test_bert_arena_closed_form(key, B, e):
-    model, args = make(key)
-    sched = build_pipeline(capture(model, args), Config())
+    sched = build_pipeline(graph_of(key), Config())
     assert sched.arena_bytes == _bert_closed_form(B, 128, e) == 1769728
     assert sched.plan.arena_bytes == sched.plan.peak_bytes
 
