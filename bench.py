@@ -240,7 +240,10 @@ def main() -> int:
                            ("fused_attention", "C2", ATTENTION),
                            ("fused_attention", "C4", ATTENTION),
                            ("all + fused_attention", "C2", ALL),
-                           ("all + fused_attention", "C4", ALL))
+                           ("all + fused_attention", "C4", ALL),
+                           # GPT-2 b32 s512 (config 5): the key-blocked attention kernel
+                           ("gpt2_b32_s512", "C5", Config()),
+                           ("gpt2_b32_s512", "C5", ALL))
     for name, key, cfg in variant_runs:
         model, inputs = make(key, "cuda")
         compiled = mlc.compile(model, inputs, cfg)
@@ -249,7 +252,11 @@ def main() -> int:
                  "kernels": compiled.schedule.counts()}
         if cfg.fused_attention:
             entry["attention_kernel"] = _attention_row(compiled, opts.kernel_iters)
-        variants.setdefault(name, {})["b1" if key == "C2" else "b32"] = entry
+        if key == "C5":
+            slot = "all + fused_attention" if cfg.fused_attention else "reference"
+        else:
+            slot = "b1" if key == "C2" else "b32"
+        variants.setdefault(name, {})[slot] = entry
         del compiled, model, inputs
         torch.cuda.empty_cache()
 

@@ -1,6 +1,9 @@
 """HIP emitter for :class:`~mlc.kernels.AttentionKernel` (gfx950 MFMA).
 
-One workgroup of ``W`` waves per (batch-head, block of ``16*W`` queries):
+Up to 128 keys, every score of a row stays in registers (below); longer rows
+use the key-blocked form (``emit_attention_blocked``) with the online-softmax
+recurrence. One workgroup of ``W`` waves per (batch-head, block of ``16*W``
+queries):
 
 * **staging**: the block's queries, and every key and value of the head,
   are copied from their strided views into LDS with 128-bit loads along
@@ -93,7 +96,7 @@ def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc:
     n = R * C // per
     trips = -(-n // threads)
     full = n % threads == 0
-    ty = "mlc::f16x8" if per == 8 else "mlc::f16"
+    ty = "mlc::half8" if per == 8 else "mlc::f16"
     load.append(f"  {ty} {tag}[{trips}];")
     load.append("#pragma unroll")
     load.append(f"  for (int u = 0; u < {trips}; ++u) {{")
@@ -117,17 +120,17 @@ def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc:
     load.append(f"    {rc}")
     store.append(f"    {rc}")
     if per == 8:
-        load.append(f"    {guard}{tag}[u] = *reinterpret_cast<const mlc::f16x8*>({addr});")
+        load.append(f"    {guard}{tag}[u] = *reinterpret_cast<const mlc::half8*>({addr});")
         if mode == "c" and pc == 1 and pr % 8 == 0:
-            store.append(f"    {guard}*reinterpret_cast<mlc::f16x8*>({lds} + r * {pr} + c) = {tag}[u];")
+            store.append(f"    {guard}*reinterpret_cast<mlc::half8*>({lds} + r * {pr} + c) = {tag}[u];")
         elif mode == "r" and pr == 1 and pc % 8 == 0:
-            store.append(f"    {guard}*reinterpret_cast<mlc::f16x8*>({lds} + r + c * {pc}) = {tag}[u];")
+            store.append(f"    {guard}*reinterpret_cast<mlc::half8*>({lds} + r + c * {pc}) = {tag}[u];")
         else:
             step_r, step_c = (0, 1) if mode == "c" else (1, 0)
             store.append(f"    {guard}{{")
             store.append("#pragma unroll")
             store.append(f"      for (int j = 0; j < 8; ++j) {lds}[(r + j * {step_r}) * {pr} + "
-                         f"(c + j * {step_c}) * {pc}] = {tag}[u].v[j];")
+                         f"(c + j * {step_c}) * {pc}] = {tag}[u][j];")
             store.append("    }")
     else:
         load.append(f"    {guard}{tag}[u] = {src}[{base} + ({it})r * ({it}){sr} + ({it})c * ({it}){sc}];")
@@ -141,7 +144,13 @@ def _aligned(offset: int, strides) -> bool:
     return offset % 8 == 0 and all(s % 8 == 0 for s in strides)
 
 
+#: the most keys whose scores one wave holds in registers (the single-pass form)
+MAX_RESIDENT_KEYS = 128
+
+
 def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
+    if k.kt.shape[2] > MAX_RESIDENT_KEYS:
+        return emit_attention_blocked(k, cfg)
     sm = k.softmax
     BH, T, D = k.q.shape
     Tk = k.kt.shape[2]
@@ -354,3 +363,288 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
                        "queries_per_wg": QB})
     return "\n".join(L), spec
 
+
+
+# --------------------------------------------------------------------------
+# key-blocked form (more keys than one workgroup holds)
+# --------------------------------------------------------------------------
+
+#: keys per block of the blocked kernel
+KEY_BLOCK = 64
+
+
+def blocked_form(sm):
+    """The online-softmax structure of ``sm`` when it is exactly
+    ``cast?(exp(x - max(x)) / sum(exp(x - max(x))))`` over its row, else None.
+    The blocked kernel needs it: it keeps a running max and sum per row and
+    rescales its partial output, instead of holding the whole row."""
+    from ..ir.scalar import Call, Cast, Ref
+    from .reduction_schedule import detect_online_softmax
+
+    online = detect_online_softmax(sm)
+    if online is None or len(sm.outputs) != 1 or sm.row_outputs:
+        return None
+    by_name = {s.name: s for s in sm.steps}
+
+    def through(e):
+        while True:
+            if isinstance(e, Ref) and isinstance(by_name.get(e.name), Bind):
+                e = by_name[e.name].expr
+            elif isinstance(e, Cast):
+                e = e.x
+            else:
+                return e
+
+    out = through(sm.out_expr[sm.outputs[0].value.name])
+    if not (isinstance(out, Call) and out.fn == "div" and isinstance(out.args[1], Ref)
+            and out.args[1].name == online.sum_step.name):
+        return None
+    if through(out.args[0]) != through(online.sum_step.expr):
+        return None
+    return online
+
+
+def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
+    """Key-blocked attention: each workgroup streams the head's keys and
+    values through LDS in blocks of ``KEY_BLOCK``, keeping per query row a
+    running max ``m`` and sum ``l`` (the online-softmax recurrence) and an
+    fp32 output accumulator rescaled by ``exp(m_old - m_new)`` per block; the
+    division by ``l`` happens once at the end. The next block's loads are in
+    flight while the current block computes."""
+    from .reduction_schedule import dependencies
+
+    sm = k.softmax
+    online = blocked_form(sm)
+    assert online is not None, "not an online-softmax reduction"
+    BH, T, D = k.q.shape
+    Tk = k.kt.shape[2]
+    KB = KEY_BLOCK
+    NB = Tk // KB
+    NT = KB // 16
+    W = attention_waves(BH, T)
+    QB = 16 * W
+    NQB = -(-T // QB)
+    THREADS = W * WAVE
+    it = index_type(k)
+    PK, PV, PQ = D + 8, KB + 8, D + 8
+    lds_bytes = 2 * (KB * PK + D * PV + QB * PQ)
+
+    L: list[str] = []
+    L.append(f"extern \"C\" __global__ void __launch_bounds__({THREADS}) "
+             f"KERNEL({', '.join(_params(k))}) {{")
+    L.append(f"  // attention, key-blocked: {BH} heads x [{T} x {D}] x [{Tk}] in {NB} blocks of "
+             f"{KB} keys; {QB} queries per workgroup, 16 per wave; online softmax")
+    L.append(f"  __shared__ __align__(16) mlc::f16 ks[{KB * PK}];")
+    L.append(f"  __shared__ __align__(16) mlc::f16 vt[{D * PV}];")
+    L.append(f"  __shared__ __align__(16) mlc::f16 qs[{QB * PQ}];")
+    L.append(f"  const {it} bh = ({it})(blockIdx.x / {NQB});")
+    L.append(f"  const int q0 = (int)(blockIdx.x % {NQB}) * {QB};")
+    ql_ = k.q.layout
+    qsb, qsr, qsc = ql_.strides
+    rows_valid = None
+    if T % QB:
+        L.append(f"  const int qn = {T} - q0 < {QB} ? {T} - q0 : {QB};")
+        rows_valid = "qn"
+    q_ld, q_st = _stage("gq", "qs", "in0",
+                        f"(({it}){ql_.offset} + bh * ({it}){qsb} + ({it})q0 * ({it}){qsr})",
+                        QB, D, qsr, qsc, PQ, 1, _aligned(ql_.offset, (qsb, qsr)),
+                        _aligned(ql_.offset, (qsb, qsc)), THREADS, rows_valid, it)
+    kl = k.kt.layout
+    ksb, ksd, ksk = kl.strides
+    k_ld, k_st = _stage("gk", "ks", "in1",
+                        f"(({it}){kl.offset} + bh * ({it}){ksb} + ({it})kb0 * ({it}){ksk})",
+                        KB, D, ksk, ksd, PK, 1, _aligned(kl.offset, (ksb, ksk, KB * ksk)),
+                        _aligned(kl.offset, (ksb, ksd, KB * ksk)), THREADS, None, it)
+    vl = k.v.layout
+    vsb, vsk, vsd = vl.strides
+    v_ld, v_st = _stage("gv", "vt", "in2",
+                        f"(({it}){vl.offset} + bh * ({it}){vsb} + ({it})kb0 * ({it}){vsk})",
+                        KB, D, vsk, vsd, 1, PV, _aligned(vl.offset, (vsb, vsk, KB * vsk)),
+                        _aligned(vl.offset, (vsb, vsd, KB * vsk)), THREADS, None, it)
+    # declarations hoisted out of the block loop
+    L += q_ld + q_st
+    L += [k_ld[0], v_ld[0]]
+    L.append("  int kb0 = 0;")
+    L += k_ld[1:] + v_ld[1:] + k_st + v_st
+    L.append("  __syncthreads();")
+    L.append("  const int w = threadIdx.x / 64, l = threadIdx.x % 64;")
+    L.append("  const int ql = l % 16, g = l / 16;")
+    L.append("  const int qw = q0 + w * 16;")
+    L.append(f"  const bool active = qw < {T};  // wave-uniform; every wave meets every barrier")
+    L.append(f"  const {it} row = bh * ({it}){T} + ({it})(active ? qw + ql : 0);")
+    L.append(f"  mlc::half8 qf[{D // 32}];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int dc = 0; dc < {D // 32}; ++dc)")
+    L.append(f"    qf[dc] = *reinterpret_cast<const mlc::half8*>(qs + (w * 16 + ql) * {PQ} + dc * 32 + g * 8);")
+    L.append("  float m_run = (-__builtin_huge_valf()), l_run = 0.0f;")
+    L.append(f"  mlc::float4v o[{D // 16}];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int dt = 0; dt < {D // 16}; ++dt) o[dt] = mlc::float4v{{0.0f, 0.0f, 0.0f, 0.0f}};")
+
+    # the reduction's operands other than the scores; row-constant ones once
+    offs = _RowOffsets(sm, it)
+    vector = varies_by_column(sm)
+    col_slots = [i for i, a in enumerate(sm.inputs) if a.index.varies_along("col")]
+    param = {}
+    n = 3
+    for i in range(len(sm.inputs)):
+        if i != k.score_slot:
+            param[i] = n
+            n += 1
+    in_types = {i: compute_type(a.dtype) for i, a in enumerate(sm.inputs)}
+    for i, a in enumerate(sm.inputs):
+        if i != k.score_slot and i not in col_slots:
+            L.append(f"  const {in_types[i]} x{i} = mlc::ld(in{param[i]} + {offs.row(a)});")
+    temp_types: dict[str, str] = {}
+
+    def ref_elem(slot):
+        if slot == k.score_slot:
+            return "s[t][i]", "float"
+        if slot in col_slots:
+            return f"x{slot}[t][i]", in_types[slot]
+        return f"x{slot}", in_types[slot]
+
+    def ref_scalar(slot):
+        if slot == k.score_slot or slot in col_slots:
+            raise AssertionError("column operand read in a row-scalar expression")
+        return f"x{slot}", in_types[slot]
+
+    def temp_elem(name):
+        return (f"{name}[t][i]" if name in vector else name), temp_types[name]
+
+    def temp_scalar(name):
+        if name in vector:
+            raise AssertionError("vector temp read in a row-scalar expression")
+        return name, temp_types[name]
+
+    R_ = _FastExpRenderer if FAST_SOFTMAX_MATH else Renderer
+    elem_r, scal_r = R_(ref_elem, temp_elem), R_(ref_scalar, temp_scalar)
+    deps = dependencies(sm.steps)
+    needed = deps[online.max_step.name]
+    by_name = {s.name: s for s in sm.steps}
+    # row-constant binds the maxed value needs, before the loop
+    for nm in [s.name for s in sm.steps if s.name in needed]:
+        st = by_name[nm]
+        if isinstance(st, Bind) and nm not in vector:
+            code, t = scal_r(st.expr)
+            temp_types[nm] = t
+            L.append(f"  const {t} {nm} = {code};")
+    exp_ = "mlc::exp_fast" if FAST_SOFTMAX_MATH else "mlc::exp_"
+
+    L.append(f"  for (int b = 0; b < {NB}; ++b) {{")
+    L.append(f"    if (b + 1 < {NB}) {{  // next block's loads, in flight during this block's math")
+    L.append(f"      kb0 = (b + 1) * {KB};")
+    L += ["    " + x for x in k_ld[1:] + v_ld[1:]]
+    L.append("    }")
+    L.append("    if (active) {")
+    L.append(f"      const int kc = b * {KB};")
+    L.append(f"      float s[{NT}][4];")
+    L.append("#pragma unroll")
+    L.append(f"      for (int t = 0; t < {NT}; ++t) {{")
+    L.append("        mlc::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};")
+    L.append("#pragma unroll")
+    L.append(f"        for (int dc = 0; dc < {D // 32}; ++dc) {{")
+    L.append(f"          const mlc::half8 kf = *reinterpret_cast<const mlc::half8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
+    L.append("          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[dc], acc, 0, 0, 0);")
+    L.append("        }")
+    L.append("#pragma unroll")
+    L.append(f"        for (int i = 0; i < 4; ++i) s[t][i] = {cast_code('acc[i]', k.score_dtype)[0]};")
+    L.append("      }")
+    for i, a in enumerate(sm.inputs):
+        if i == k.score_slot or i not in col_slots:
+            continue
+        acc = _row_col_access(sm, a, 4)
+        p = param[i]
+        L.append(f"      {in_types[i]} x{i}[{NT}][4];")
+        L.append(f"      {{ const {it} rb = {offs.row(a)};")
+        L.append("#pragma unroll")
+        L.append(f"        for (int t = 0; t < {NT}; ++t) {{")
+        L.append(f"          const {it} c0 = ({it})(kc + t * 16 + g * 4);")
+        if acc.mode == "affine" and acc.aligned:
+            L.append(f"          mlc::load_pack<4>(x{i}[t], in{p} + rb + {offs.col(a, 'c0')});")
+        else:
+            L.append("#pragma unroll")
+            L.append(f"          for (int j = 0; j < 4; ++j) x{i}[t][j] = "
+                     f"mlc::ld(in{p} + rb + {offs.col(a, '(c0 + (' + it + ')j)')});")
+        L.append("        }")
+        L.append("      }")
+    for nm in [s.name for s in sm.steps if s.name in needed]:
+        st = by_name[nm]
+        if isinstance(st, Bind) and nm in vector:
+            code, t = elem_r(st.expr)
+            temp_types[nm] = t
+            L.append(f"      {t} {nm}[{NT}][4];")
+            L.append("#pragma unroll")
+            L.append(f"      for (int t = 0; t < {NT}; ++t)")
+            L.append("#pragma unroll")
+            L.append(f"        for (int i = 0; i < 4; ++i) {nm}[t][i] = {code};")
+    xcode, _ = elem_r(online.value)
+    L.append(f"      float x[{NT}][4];")
+    L.append("      float mb = (-__builtin_huge_valf());")
+    L.append("#pragma unroll")
+    L.append(f"      for (int t = 0; t < {NT}; ++t)")
+    L.append("#pragma unroll")
+    L.append("        for (int i = 0; i < 4; ++i) {")
+    L.append(f"          x[t][i] = (float)({xcode});")
+    L.append("          mb = mlc::max_<float>(mb, x[t][i]);")
+    L.append("        }")
+    L.append("      mb = mlc::max_<float>(mb, __shfl_xor(mb, 16, 64));")
+    L.append("      mb = mlc::max_<float>(mb, __shfl_xor(mb, 32, 64));")
+    L.append("      const float m_new = mlc::max_<float>(m_run, mb);")
+    L.append(f"      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : {exp_}(m_run - m_new);")
+    L.append("      const bool none = m_new == (-__builtin_huge_valf());")
+    L.append(f"      mlc::half4 p[{NT}];")
+    L.append("      float psum = 0.0f;")
+    L.append("#pragma unroll")
+    L.append(f"      for (int t = 0; t < {NT}; ++t)")
+    L.append("#pragma unroll")
+    L.append("        for (int i = 0; i < 4; ++i) {")
+    L.append(f"          const float e = none ? 0.0f : {exp_}(x[t][i] - m_new);")
+    L.append("          psum += e;")
+    L.append(f"          p[t][i] = (mlc::f16)e;")
+    L.append("        }")
+    L.append("      l_run = l_run * alpha + psum;")
+    L.append("      m_run = m_new;")
+    L.append("#pragma unroll")
+    L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt) {{")
+    L.append("        o[dt] *= alpha;")
+    L.append(f"        const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 4;")
+    L.append("#pragma unroll")
+    L.append(f"        for (int m = 0; m < {NT // 2}; ++m) {{")
+    L.append("          const mlc::half4 lo = *reinterpret_cast<const mlc::half4*>(vrow + m * 32);")
+    L.append("          const mlc::half4 hi = *reinterpret_cast<const mlc::half4*>(vrow + m * 32 + 16);")
+    L.append("          const mlc::half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};")
+    L.append("          const mlc::half8 bq = {p[2 * m][0], p[2 * m][1], p[2 * m][2], p[2 * m][3], "
+             "p[2 * m + 1][0], p[2 * m + 1][1], p[2 * m + 1][2], p[2 * m + 1][3]};")
+    L.append("          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, o[dt], 0, 0, 0);")
+    L.append("        }")
+    L.append("      }")
+    L.append("    }")
+    L.append("    __syncthreads();  // every wave is done with this block's tiles")
+    L.append(f"    if (b + 1 < {NB}) {{")
+    L += ["    " + x for x in k_st + v_st]
+    L.append("    }")
+    L.append("    __syncthreads();")
+    L.append("  }")
+    L.append("  if (!active) return;")
+    L.append("  l_run += __shfl_xor(l_run, 16, 64);")
+    L.append("  l_run += __shfl_xor(l_run, 32, 64);")
+    div = "* inv" if FAST_SOFTMAX_MATH else "/ l_run"
+    if FAST_SOFTMAX_MATH:
+        L.append("  const float inv = 1.0f / l_run;")
+    omap = k.outputs[0].index
+    parts = render_terms(axis_terms(omap, "idx"), BH * T * D, "f0", it)
+    if omap.base:
+        parts.append(f"({it}){omap.base}")
+    L.append("#pragma unroll")
+    L.append(f"  for (int dt = 0; dt < {D // 16}; ++dt) {{")
+    L.append(f"    const mlc::half4 h = {{(mlc::f16)(o[dt][0] {div}), (mlc::f16)(o[dt][1] {div}), "
+             f"(mlc::f16)(o[dt][2] {div}), (mlc::f16)(o[dt][3] {div})}};")
+    L.append(f"    const {it} f0 = row * ({it}){D} + ({it})(dt * 16 + g * 4);")
+    L.append(f"    *reinterpret_cast<mlc::half4*>(out0 + {join_offset(parts, it)}) = h;")
+    L.append("  }")
+    L.append("}")
+    spec = LaunchSpec("", BH * NQB, THREADS, lds_bytes,
+                      {"kind": "attention", "mode": "blocked", "heads": BH, "queries": T,
+                       "keys": Tk, "head_dim": D, "queries_per_wg": QB, "key_block": KB})
+    return "\n".join(L), spec

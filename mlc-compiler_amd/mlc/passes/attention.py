@@ -12,9 +12,13 @@ rendered inside it.
 Applies when the scores feed only the reduction, the reduction reads them at
 identity over a ``[BH*T] x [Tk]`` frame and writes only the probabilities,
 those feed only the second ``bmm`` as its first operand, scores,
-probabilities and output are contiguous, and the shapes fit one workgroup:
-T a multiple of 16 and Tk a multiple of 32, both up to 128, head size a
-multiple of 32 up to 128, fp16 operands (the MFMA the kernel is built on).
+probabilities and output are contiguous, T is a multiple of 16, the head size
+a multiple of 32 up to 128, and the operands fp16 (the MFMA the kernel is
+built on). Up to 128 keys (a multiple of 32) every score of a row stays in
+registers and the reduction's own steps are rendered, whatever they are.
+Longer rows (a multiple of 64 keys) are streamed in key blocks with the
+online-softmax recurrence, which needs the reduction to be exactly a softmax
+(``exp(x - max) / sum``) of a per-element value ``x``.
 
 When K or V is written by one of this compiler's pointwise kernels for the
 attention alone, that kernel is re-derived to write K as ``[bh][key][d]``
@@ -31,6 +35,7 @@ from dataclasses import replace
 
 import torch
 
+from ..codegen.hip_attention import KEY_BLOCK, blocked_form
 from ..codegen.index import flat_index
 from ..ir.graph import Value
 from ..ir.types import Layout
@@ -38,7 +43,10 @@ from ..kernels import (AttentionKernel, ExternKernel, KernelArg, PointwiseKernel
                        ReductionKernel, Schedule)
 from .layout import is_pure_copy, compose
 
+#: keys held in registers by the single-pass kernel; longer rows are key-blocked
 MAX_SEQ = 128
+#: the key-blocked kernel's limit (keys are streamed; this bounds the row index math)
+MAX_KEYS = 1 << 16
 MAX_HEAD = 128
 
 
@@ -234,8 +242,14 @@ def _match(kernels, i, readers, graph_outputs):
     Tk = kt.shape[2]
     if kt.shape != (BH, D, Tk) or v.shape != (BH, Tk, D) or s_val.shape != (BH, T, Tk):
         return None
-    if not (T % 16 == 0 and Tk % 32 == 0 and T <= MAX_SEQ and Tk <= MAX_SEQ
-            and D % 32 == 0 and D <= MAX_HEAD):
+    if not (T % 16 == 0 and D % 32 == 0 and D <= MAX_HEAD):
+        return None
+    if Tk > MAX_SEQ:
+        # the key-blocked kernel: whole key blocks, and a softmax it can
+        # evaluate with the online recurrence
+        if Tk % KEY_BLOCK or Tk > MAX_KEYS or blocked_form(kernels[j]) is None:
+            return None
+    elif Tk % 32:
         return None
     dt = q.dtype
     if dt != torch.float16 or any(x.dtype != dt for x in (kt, v, o_val, s_val, prob)):

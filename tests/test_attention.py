@@ -40,6 +40,15 @@ class ScoresOut(Attention):
         return scores.softmax(dim=-1) @ v, scores
 
 
+class LogSoftmax(Attention):
+    """Not an ``exp(x - max) / sum`` row: only the single-pass kernel, which
+    renders any reduction, could take it."""
+
+    def forward(self, q, k, v, mask):
+        scores = (q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1]) + mask
+        return torch.log_softmax(scores.float(), dim=-1).to(q.dtype) @ v
+
+
 def _inputs(b, h, t, tk, d, dtype=torch.float16, seed=0):
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(b, h, t, d, generator=g).to(dtype)
@@ -57,7 +66,7 @@ def _attention(sched):
                                        ("C3", Config(fused_attention=True), 12),
                                        ("C4", Config(fused_attention=True), 12),
                                        ("C2", ALL, 12), ("C4", ALL, 12),
-                                       ("C5", Config(fused_attention=True), 0),
+                                       ("C5", Config(fused_attention=True), 12),
                                        ("C1", Config(fused_attention=True), 0)])
 def test_workloads_fuse_every_layer(key, cfg, n):
     base = build_pipeline(graph_of(key), Config())
@@ -76,8 +85,11 @@ def test_workloads_fuse_every_layer(key, cfg, n):
 def test_refused_when_scores_escape_or_shapes_do_not_fit():
     q, k, v, m = _inputs(1, 2, 32, 32, 64)
     assert len(_attention(build_pipeline(capture(ScoresOut(), (q, k, v, m)), ATTN))) == 0
-    q, k, v, m = _inputs(1, 2, 160, 160, 64)  # longer than one workgroup holds
+    q, k, v, m = _inputs(1, 2, 160, 160, 64)  # too long to hold, not whole 64-key blocks
     assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
+    q, k, v, m = _inputs(1, 2, 32, 256, 64)  # key-blocked, but not a softmax
+    assert len(_attention(build_pipeline(capture(LogSoftmax(), (q, k, v, m)), ATTN))) == 0
+    assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 1
     q, k, v, m = _inputs(1, 2, 32, 32, 64, torch.float32)
     assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
     q, k, v, m = _inputs(1, 2, 32, 48, 64)  # keys not a multiple of 32
@@ -86,7 +98,8 @@ def test_refused_when_scores_escape_or_shapes_do_not_fit():
     assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
 
 
-@pytest.mark.parametrize("shape", [(2, 3, 32, 32, 64), (1, 2, 80, 96, 32), (1, 1, 16, 128, 128)])
+@pytest.mark.parametrize("shape", [(2, 3, 32, 32, 64), (1, 2, 80, 96, 32), (1, 1, 16, 128, 128),
+                                   (1, 2, 48, 256, 64), (2, 1, 16, 192, 32)])
 def test_oracle_fused_attention_matches_float64(shape):
     """The oracle's fused kernel (fp32 products rounded to fp16 scores, the
     reduction's steps, fp16 probabilities, fp32 products) against attention
@@ -130,7 +143,7 @@ def test_generated_kernel_shape():
     assert body.count("__builtin_amdgcn_mfma_f32_16x16x32_f16") == 2
     assert "__syncthreads();" in body and body.index("__syncthreads();") < body.index("return;")
     # C2's merged-qkv views are unit-stride along the head dim: 128-bit LDS stores
-    assert body.count("*reinterpret_cast<mlc::f16x8*>(") == 2
+    assert body.count("*reinterpret_cast<mlc::half8*>(") == 2
 
 
 def test_attention_module_cross_compiles_for_gfx950(tmp_path, monkeypatch):
@@ -153,7 +166,7 @@ def test_operand_producers_write_the_mfma_layouts():
         assert a.kt.layout.strides == (128 * 64, 1, 64)
         assert a.v.layout.strides == (128 * 64, 1, 128)
         body = mod.functions[mod.launches[a.name].symbol]
-        assert body.count("*reinterpret_cast<mlc::f16x8*>(") == 3 and ".v[j]" not in body
+        assert body.count("*reinterpret_cast<mlc::half8*>(") == 3 and "[u][j]" not in body
     assert not verify(list(sched.plan.live_ranges.values()), sched.plan.offsets)
 
 
@@ -192,3 +205,20 @@ def test_context_copy_folds_into_the_attention_stores():
         want = model(*args)
     got = compile_reference(model, args, ATTN)(*args)
     torch.testing.assert_close(got.float(), want.float(), rtol=1e-2, atol=5e-2)
+
+
+def test_long_rows_use_the_key_blocked_kernel():
+    """GPT-2 b32 s512 (512 keys) is key-blocked: 64-key blocks streamed
+    through LDS, next block's loads in flight, one division by the row sum at
+    the end; the scores and probabilities (201 MB each per layer) are gone
+    from the arena."""
+    base = build_pipeline(graph_of("C5"), Config())
+    sched = build_pipeline(graph_of("C5"), Config(fused_attention=True))
+    mod = generate_module(sched, Config(fused_attention=True))
+    att = _attention(sched)
+    spec = mod.launches[att[0].name]
+    assert spec.meta["mode"] == "blocked" and spec.meta["key_block"] == 64
+    body = mod.functions[spec.symbol]
+    assert "m_run" in body and "l_run" in body and "mlc::exp_fast" in body
+    assert body.count("__syncthreads();") == 3
+    assert sched.arena_bytes < base.arena_bytes // 2

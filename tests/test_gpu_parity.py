@@ -409,15 +409,20 @@ def test_arena_is_one_slab_with_planned_offsets():
 
 
 @pytest.mark.parametrize("shape", [(2, 3, 32, 32, 64), (1, 2, 80, 96, 32), (1, 1, 16, 128, 128),
-                                   (3, 2, 128, 128, 64), (1, 4, 48, 64, 64)],
+                                   (3, 2, 128, 128, 64), (1, 4, 48, 64, 64),
+                                   (1, 2, 48, 256, 64), (2, 1, 16, 192, 32),
+                                   (1, 4, 128, 512, 64), (1, 1, 80, 320, 128)],
                          ids=["b2h3-32x32-d64", "80x96-d32-partial-block", "16x128-d128",
-                              "b3h2-128x128-d64", "48x64-partial-block"])
+                              "b3h2-128x128-d64", "48x64-partial-block", "48x256-key-blocked",
+                              "16x192-d32-key-blocked", "128x512-key-blocked",
+                              "80x320-d128-key-blocked-partial"])
 def test_fused_attention_shapes(shape):
-    """The MFMA attention kernel over shapes that exercise its edges: a
-    partial query block (80 queries, 64 per workgroup), more keys than
-    queries, head sizes 32 and 128, fewer than four waves. Against the
-    oracle's fused kernel on the same inputs and against float64 attention:
-    within 2e-3 of the largest output."""
+    """The MFMA attention kernels over shapes that exercise their edges: a
+    partial query block, more keys than queries, head sizes 32 and 128, fewer
+    than four waves, and more than 128 keys (the key-blocked kernel, 64-key
+    blocks with the online-softmax recurrence). Against the oracle's fused
+    kernel on the same inputs and against float64 attention: within 2e-3 of
+    the largest output."""
     from test_attention import Attention, _inputs
 
     args = _inputs(*shape)
@@ -456,3 +461,46 @@ def test_fused_attention_matches_reference_schedule(key):
           f"schedule {err_eager:.2e}), vs float64 {err_truth:.2e}")
     assert err_truth <= 2e-3
     assert err <= max(2e-3, err_eager)
+
+
+def test_fused_attention_config5_first_block_lockstep():
+    """GPT-2 b32 s512's first transformer block with fused (key-blocked)
+    attention, each kernel fed the oracle's own inputs: fp16 outputs within
+    2e-3 of the largest magnitude."""
+    from mlc.kernels import AttentionKernel
+
+    model, args = make("C5", "cpu")
+    graph = capture(model, args)
+    schedule = build_pipeline(graph, ATTN)
+    first = next(i for i, k in enumerate(schedule.kernels) if isinstance(k, AttentionKernel))
+    rt = HipRuntime(schedule, ATTN, torch.device("cuda:0"))
+    assert rt.launch_table[schedule.kernels[first].name].meta["mode"] == "blocked"
+    worst = {}
+
+    def check(k, name, got, want):
+        err = rel_err(got, want)
+        worst[k.name] = err
+        assert err <= 2e-3, f"{k.summary()}: output {name} rel err {err:.3e}"
+
+    lockstep(schedule, graph, _params_by_buffer(graph), args, rt, check, limit=first + 1)
+    print("C5 first block with fused attention: worst per-kernel rel err", max(worst.values()))
+
+
+def test_fused_attention_config5_full_size():
+    """GPT-2 b32 s512 at full size with fused attention against the reference
+    schedule: logits finite, and no farther from the reference schedule than
+    eager PyTorch is (or 2e-3)."""
+    gm, ga = make("C5", "cuda")
+    ref = mlc.compile(gm, ga, Config())(*ga).clone()
+    compiled = mlc.compile(gm, ga, ATTN)
+    assert compiled.schedule.counts()["attention"] == 12
+    got = compiled(*ga)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    with torch.no_grad():
+        eager = gm(*ga)
+    err, err_eager = rel_err(got, ref), rel_err(eager, ref)
+    print(f"C5 fused attention: vs reference schedule {err:.2e}, eager vs reference schedule "
+          f"{err_eager:.2e}")
+    assert err <= max(2e-3, err_eager)
+    del ref, got, eager, compiled
