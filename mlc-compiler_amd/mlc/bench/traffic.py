@@ -17,7 +17,8 @@ It launches, ``--iters`` times each:
    on (``merge_parallel_gemms``, ``gemm_epilogue``, ``layout_selection``,
    ``fused_attention``); with ``--kernel all``, every generated kernel of
    the reference schedule at config 4 (for per-kernel counters such as
-   ``SQ_INSTS_VALU``).
+   ``SQ_INSTS_VALU``). ``--workload`` picks another configuration (default
+   config 4).
 
 It prints each kernel's symbol and algorithmic bytes per launch so the
 counter CSV can be matched to them.
@@ -40,6 +41,7 @@ def main() -> int:
     ap.add_argument("--iters", type=int, default=5)
     ap.add_argument("--copy-mib", type=int, default=1024)
     ap.add_argument("--kernel", choices=("gelu", "attention", "all"), default="gelu")
+    ap.add_argument("--workload", default="C4", help="workload key (default C4)")
     opts = ap.parse_args()
 
     import torch
@@ -60,7 +62,7 @@ def main() -> int:
     torch.cuda.synchronize()
     print(f"copy: {2 * n} bytes read + {2 * n} bytes written per launch", flush=True)
 
-    model, inputs = make("C4", "cuda")
+    model, inputs = make(opts.workload, "cuda")
     if opts.kernel == "gelu":
         cfg = Config(cuda_graphs=False)
 

@@ -44,9 +44,11 @@ from .hip_backend import (_IDENTITY, _OP, WAVE, LaunchSpec, Renderer, _RowOffset
 from .reduction_schedule import varies_by_column
 
 #: the softmax's exp and its division by the row sum in fast forms
-#: (``mlc::exp_fast`` and a multiply by the row reciprocal). Both are used only
-#: here, where every probability is rounded to fp16 before it is used: their
-#: errors (about 1e-6 and 1.5 fp32 ulp) are far below that rounding.
+#: (``mlc::exp_fast`` and a multiply by the row reciprocal), and floating-point
+#: contraction inside the attention kernels (a scale and a mask add become one
+#: mixed-precision FMA on the fp16 operands). All of it is used only here, where
+#: every probability is rounded to fp16 before it is used: the errors (about
+#: 1e-6, 1.5 fp32 ulp, one fp32 rounding) are far below that rounding.
 FAST_SOFTMAX_MATH = True
 
 #: waves per workgroup (each owns 16 queries): ``waves`` forces a count;
@@ -168,6 +170,8 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
              f"KERNEL({', '.join(_params(k))}) {{")
     L.append(f"  // attention: {BH} heads x [{T} x {D}] x [{Tk}]; {QB} queries per workgroup, "
              f"16 per wave")
+    if FAST_SOFTMAX_MATH:
+        L.append("#pragma clang fp contract(fast)")
     L.append(f"  __shared__ __align__(16) mlc::f16 ks[{Tk * PK}];")
     L.append(f"  __shared__ __align__(16) mlc::f16 vt[{D * PV}];")
     L.append(f"  __shared__ __align__(16) mlc::f16 qs[{QB * PQ}];")
@@ -434,6 +438,8 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
              f"KERNEL({', '.join(_params(k))}) {{")
     L.append(f"  // attention, key-blocked: {BH} heads x [{T} x {D}] x [{Tk}] in {NB} blocks of "
              f"{KB} keys; {QB} queries per workgroup, 16 per wave; online softmax")
+    if FAST_SOFTMAX_MATH:
+        L.append("#pragma clang fp contract(fast)")
     L.append(f"  __shared__ __align__(16) mlc::f16 ks[{KB * PK}];")
     L.append(f"  __shared__ __align__(16) mlc::f16 vt[{D * PV}];")
     L.append(f"  __shared__ __align__(16) mlc::f16 qs[{QB * PQ}];")
@@ -590,16 +596,20 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("        }")
     L.append("      mb = mlc::max_<float>(mb, __shfl_xor(mb, 16, 64));")
     L.append("      mb = mlc::max_<float>(mb, __shfl_xor(mb, 32, 64));")
+    L.append("      // a block whose scores are all -inf for every row of the wave (a causal")
+    L.append("      // mask's upper triangle) adds exactly nothing: skip its exp and P.V")
+    L.append("      if (!__all(mb == (-__builtin_huge_valf()))) {")
     L.append("      const float m_new = mlc::max_<float>(m_run, mb);")
     L.append(f"      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : {exp_}(m_run - m_new);")
-    L.append("      const bool none = m_new == (-__builtin_huge_valf());")
+    L.append("      // a row with no finite score yet subtracts 0: its x are all -inf, exp gives 0")
+    L.append("      const float m_sub = m_new == (-__builtin_huge_valf()) ? 0.0f : m_new;")
     L.append(f"      mlc::half4 p[{NT}];")
     L.append("      float psum = 0.0f;")
     L.append("#pragma unroll")
     L.append(f"      for (int t = 0; t < {NT}; ++t)")
     L.append("#pragma unroll")
     L.append("        for (int i = 0; i < 4; ++i) {")
-    L.append(f"          const float e = none ? 0.0f : {exp_}(x[t][i] - m_new);")
+    L.append(f"          const float e = {exp_}(x[t][i] - m_sub);")
     L.append("          psum += e;")
     L.append(f"          p[t][i] = (mlc::f16)e;")
     L.append("        }")
@@ -618,6 +628,7 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
              "p[2 * m + 1][0], p[2 * m + 1][1], p[2 * m + 1][2], p[2 * m + 1][3]};")
     L.append("          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, o[dt], 0, 0, 0);")
     L.append("        }")
+    L.append("      }")
     L.append("      }")
     L.append("    }")
     L.append("    __syncthreads();  // every wave is done with this block's tiles")
