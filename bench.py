@@ -202,7 +202,7 @@ def main() -> int:
     import torch
 
     import mlc
-    from mlc.bench.roofline import HBM_PEAK_GBS
+    from mlc.bench.roofline import HBM_PEAK_GBS, forward_bytes
     from mlc.bench.workloads import make
     from mlc.config import Config
 
@@ -216,6 +216,7 @@ def main() -> int:
         results[key]["kernels"] = compiled.schedule.counts()
         results[key]["graph_nodes"] = compiled._module.graph_nodes()
         results[key]["arena_bytes"] = compiled.schedule.arena_bytes
+        results[key]["forward_bytes"] = forward_bytes(compiled.schedule)
         if key == "C4":
             tables[key] = _kernel_table(compiled, opts.kernel_iters)
         print(f"# {key}: {results[key]}", file=sys.stderr, flush=True)
@@ -303,6 +304,13 @@ def main() -> int:
                                                      "graph_nodes", "arena_bytes")}},
         },
         "schedule_variants": variants,
+        # the whole forward (library GEMMs included) against its bytes-moved floor
+        "e2e_roofline": {
+            b: {"algorithmic_bytes": results[key]["forward_bytes"],
+                "floor_ms": round(results[key]["forward_bytes"] / (HBM_PEAK_GBS * 1e6), 4),
+                "frac": round(results[key]["forward_bytes"] / (HBM_PEAK_GBS * 1e6)
+                              / results[key]["ms_per_step"], 4)}
+            for b, key in (("b1", "C2"), ("b32", "C4"))},
         "roofline": {
             "bound": "hbm",
             "kernel": f"{dom_sym}: {dom['kernel'].summary().split(': ', 1)[1]} (b32)",

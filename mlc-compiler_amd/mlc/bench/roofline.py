@@ -55,3 +55,32 @@ def algorithmic_bytes(k) -> int:
     for a in k.outputs:
         total += distinct_elements(a.index) * _itemsize(a.dtype)
     return total
+
+
+def extern_bytes(k: ExternKernel) -> int:
+    """Algorithmic bytes of a library call: every distinct operand view read
+    once (a GEMM's weights included) plus every output written once."""
+    seen = set()
+    total = 0
+    for v in k.inputs:
+        key = (v.buffer.name, v.layout)
+        if key in seen:
+            continue
+        seen.add(key)
+        total += v.numel * _itemsize(v.dtype)
+    for v in k.outputs:
+        total += v.numel * _itemsize(v.dtype)
+    return total
+
+
+def forward_bytes(schedule) -> int:
+    """Algorithmic bytes of one whole forward: every kernel, generated or
+    library, at its algorithmic traffic. Divided by the HBM peak it is the
+    bytes-moved floor of the forward's latency."""
+    total = 0
+    for k in schedule.kernels:
+        if isinstance(k, ExternKernel) and k.node.op != "aten.embedding.default":
+            total += extern_bytes(k)
+        else:
+            total += algorithmic_bytes(k)
+    return total
