@@ -27,6 +27,8 @@ CONFIGS = {
                         cuda_graphs=False),
     "all_passes": Config(cuda_graphs=False),
     "streamed": Config(max_persistent_row=4, cuda_graphs=False),
+    "every_variant": Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True,
+                            fused_attention=True, cuda_graphs=False),
 }
 
 
@@ -117,7 +119,8 @@ def test_view_layouts_match_torch(seed):
 def test_schedule_invariants(name, cname):
     """One writer per buffer; every read is of a graph input, a parameter or a
     buffer an earlier kernel wrote; views never allocate (reference
-    ``tests/test_fusion.py:51-76``, ``tests/test_capture.py:37-45``)."""
+    ``tests/test_fusion.py:51-76``, ``tests/test_capture.py:37-45``). Also
+    under every schedule variant, whose passes rewrite the schedule."""
     _, model, args = next(t for t in all_models() if t[0] == name)
     graph = capture(model, args)
     for n in graph.nodes:
@@ -200,3 +203,16 @@ def test_pointwise_tail_path_only_when_packs_do_not_divide(n, tail):
     src, spec = emit_pointwise(k)
     assert spec.meta["vec"] == 8
     assert ("if (e0 + V <= N)" in src) == tail
+
+
+@pytest.mark.parametrize("name", [m[0] for m in all_models()])
+def test_every_variant_matches_eager_on_toy_models(name):
+    """The schedule variants compute the same function: every toy model with
+    all of them on, through the oracle, against eager at the fp32 bar."""
+    _, model, args = next(t for t in all_models() if t[0] == name)
+    with torch.no_grad():
+        want = model(*args)
+    got = compile_reference(model, args, CONFIGS["every_variant"])(*args)
+    for g, w in zip(got if isinstance(got, (list, tuple)) else [got],
+                    want if isinstance(want, (list, tuple)) else [want]):
+        torch.testing.assert_close(g, w, rtol=1e-5, atol=1e-6)
