@@ -21,8 +21,9 @@ queries):
   reduce is a lane-local loop plus two ``__shfl_xor`` (16, 32).
 * **values**: ``O^T = V^T P^T`` on the same MFMA. The score layout of lane
   ``l`` is exactly the B fragment of ``P^T`` when the 32-element k axis of an
-  MFMA pairs two 16-key tiles, so probabilities never leave registers; A is
-  read from the transposed V tile with two ``ds_read_b64``. Lane ``l`` ends
+  MFMA pairs two 16-key tiles, so probabilities never leave registers. The
+  staged V^T tile stores each 32-key chunk in the key order ``mlc::vperm``
+  gives, so a lane's 8 A values are one 16-byte LDS read. Lane ``l`` ends
   with four consecutive head-dim values of query ``l % 16``: one 8-byte
   store each, at the output's index map over the flat ``[BH, T, D]`` index
   (identity, or the permutation of a folded context copy).
@@ -81,12 +82,15 @@ class _FastExpRenderer(Renderer):
 
 def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc: int, pr: int,
            pc: int, aligned_c: bool, aligned_r: bool, threads: int, rows_valid: str | None,
-           it: str) -> tuple[list[str], list[str]]:
-    """Copy the R x C tile ``src[base + r*sr + c*sc]`` to ``lds[r*pr + c*pc]``.
+           it: str, perm_r: bool = False) -> tuple[list[str], list[str]]:
+    """Copy the R x C tile ``src[base + r*sr + c*sc]`` to ``lds[r*pr + c*pc]``
+    (``lds[vperm(r) + c*pc]`` with ``perm_r``, for the V^T tile).
 
     Returns (load lines, store lines): every load of every operand is issued
     before the first LDS store, so the workgroup waits for memory once, not
     once per loop trip."""
+    assert not perm_r or pr == 1
+    rr = "mlc::vperm(r)" if perm_r else "r"
     load: list[str] = []
     store: list[str] = []
     if sc == 1 and C % 8 == 0 and aligned_c:
@@ -125,18 +129,27 @@ def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc:
         load.append(f"    {guard}{tag}[u] = *reinterpret_cast<const mlc::half8*>({addr});")
         if mode == "c" and pc == 1 and pr % 8 == 0:
             store.append(f"    {guard}*reinterpret_cast<mlc::half8*>({lds} + r * {pr} + c) = {tag}[u];")
+        elif mode == "r" and pr == 1 and pc % 8 == 0 and perm_r:
+            # 8 keys starting at a multiple of 8 land as two runs of 4
+            store.append(f"    {guard}{{")
+            store.append(f"      *reinterpret_cast<mlc::half4*>({lds} + mlc::vperm(r) + c * {pc}) = {tag}[u].lo;")
+            store.append(f"      *reinterpret_cast<mlc::half4*>({lds} + mlc::vperm(r + 4) + c * {pc}) = {tag}[u].hi;")
+            store.append("    }")
         elif mode == "r" and pr == 1 and pc % 8 == 0:
             store.append(f"    {guard}*reinterpret_cast<mlc::half8*>({lds} + r + c * {pc}) = {tag}[u];")
         else:
-            step_r, step_c = (0, 1) if mode == "c" else (1, 0)
+            if mode == "c":  # one row, 8 columns
+                row, col = rr, "(c + j)"
+            else:  # 8 rows, one column
+                row, col = ("mlc::vperm(r + j)" if perm_r else "(r + j)"), "c"
             store.append(f"    {guard}{{")
             store.append("#pragma unroll")
-            store.append(f"      for (int j = 0; j < 8; ++j) {lds}[(r + j * {step_r}) * {pr} + "
-                         f"(c + j * {step_c}) * {pc}] = {tag}[u][j];")
+            store.append(f"      for (int j = 0; j < 8; ++j) {lds}[{row} * {pr} + {col} * {pc}] "
+                         f"= {tag}[u][j];")
             store.append("    }")
     else:
         load.append(f"    {guard}{tag}[u] = {src}[{base} + ({it})r * ({it}){sr} + ({it})c * ({it}){sc}];")
-        store.append(f"    {guard}{lds}[r * {pr} + c * {pc}] = {tag}[u];")
+        store.append(f"    {guard}{lds}[{rr} * {pr} + c * {pc}] = {tag}[u];")
     load.append("  }")
     store.append("  }")
     return load, store
@@ -199,7 +212,7 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     vsb, vsk, vsd = vl.strides
     v_ld, v_st = _stage("gv", "vt", "in2", f"(({it}){vl.offset} + bh * ({it}){vsb})", Tk, D, vsk,
                         vsd, 1, PV, _aligned(vl.offset, (vsb, vsk)),
-                        _aligned(vl.offset, (vsb, vsd)), THREADS, None, it)
+                        _aligned(vl.offset, (vsb, vsd)), THREADS, None, it, perm_r=True)
     L += q_ld + k_ld + v_ld + q_st + k_st + v_st
     L.append("  __syncthreads();")
     L.append("  const int w = threadIdx.x / 64, l = threadIdx.x % 64;")
@@ -342,12 +355,10 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     L.append("#pragma unroll")
     L.append(f"  for (int dt = 0; dt < {D // 16}; ++dt) {{")
     L.append("    mlc::float4v o = {0.0f, 0.0f, 0.0f, 0.0f};")
-    L.append(f"    const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 4;")
+    L.append(f"    const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
     L.append("#pragma unroll")
     L.append(f"    for (int m = 0; m < {NT // 2}; ++m) {{")
-    L.append("      const mlc::half4 lo = *reinterpret_cast<const mlc::half4*>(vrow + m * 32);")
-    L.append("      const mlc::half4 hi = *reinterpret_cast<const mlc::half4*>(vrow + m * 32 + 16);")
-    L.append("      const mlc::half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};")
+    L.append("      const mlc::half8 a = *reinterpret_cast<const mlc::half8*>(vrow + m * 32);")
     L.append("      const mlc::half8 b = {(mlc::f16)pr[2 * m][0], (mlc::f16)pr[2 * m][1], "
              "(mlc::f16)pr[2 * m][2], (mlc::f16)pr[2 * m][3], (mlc::f16)pr[2 * m + 1][0], "
              "(mlc::f16)pr[2 * m + 1][1], (mlc::f16)pr[2 * m + 1][2], (mlc::f16)pr[2 * m + 1][3]};")
@@ -466,7 +477,8 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     v_ld, v_st = _stage("gv", "vt", "in2",
                         f"(({it}){vl.offset} + bh * ({it}){vsb} + ({it})kb0 * ({it}){vsk})",
                         KB, D, vsk, vsd, 1, PV, _aligned(vl.offset, (vsb, vsk, KB * vsk)),
-                        _aligned(vl.offset, (vsb, vsd, KB * vsk)), THREADS, None, it)
+                        _aligned(vl.offset, (vsb, vsd, KB * vsk)), THREADS, None, it,
+                        perm_r=True)
     # declarations hoisted out of the block loop
     L += q_ld + q_st
     L += [k_ld[0], v_ld[0]]
@@ -618,12 +630,10 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("#pragma unroll")
     L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt) {{")
     L.append("        o[dt] *= alpha;")
-    L.append(f"        const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 4;")
+    L.append(f"        const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
     L.append("#pragma unroll")
     L.append(f"        for (int m = 0; m < {NT // 2}; ++m) {{")
-    L.append("          const mlc::half4 lo = *reinterpret_cast<const mlc::half4*>(vrow + m * 32);")
-    L.append("          const mlc::half4 hi = *reinterpret_cast<const mlc::half4*>(vrow + m * 32 + 16);")
-    L.append("          const mlc::half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};")
+    L.append("          const mlc::half8 a = *reinterpret_cast<const mlc::half8*>(vrow + m * 32);")
     L.append("          const mlc::half8 bq = {p[2 * m][0], p[2 * m][1], p[2 * m][2], p[2 * m][3], "
              "p[2 * m + 1][0], p[2 * m + 1][1], p[2 * m + 1][2], p[2 * m + 1][3]};")
     L.append("          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, o[dt], 0, 0, 0);")

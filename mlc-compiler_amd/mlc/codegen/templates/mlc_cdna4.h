@@ -74,6 +74,13 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 struct alignas(16) f16x8 { f16 v[8]; };
 
+// Key position inside a staged V^T row of the attention kernels: within each
+// 32-key chunk, key 16h + 4g + i sits at 8g + 4h + i, so the 8 keys one lane
+// feeds an MFMA (keys 4g..4g+3 of two 16-key tiles) are one 16-byte LDS read.
+__device__ __forceinline__ int vperm(int k) {
+  return (k & ~31) | (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
+}
+
 __device__ __forceinline__ float round_f16(float x) { return static_cast<float>(static_cast<f16>(x)); }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 

@@ -166,7 +166,11 @@ def test_operand_producers_write_the_mfma_layouts():
         assert a.kt.layout.strides == (128 * 64, 1, 64)
         assert a.v.layout.strides == (128 * 64, 1, 128)
         body = mod.functions[mod.launches[a.name].symbol]
-        assert body.count("*reinterpret_cast<mlc::half8*>(") == 3 and "[u][j]" not in body
+        # Q and K: one 128-bit store per pack; V^T: two 64-bit stores at the
+        # key-permuted positions the 128-bit MFMA-operand reads expect
+        assert body.count("*reinterpret_cast<mlc::half8*>(") == 2 and "[u][j]" not in body
+        assert body.count("*reinterpret_cast<mlc::half4*>(vt + mlc::vperm(") == 2
+        assert body.count("*reinterpret_cast<const mlc::half8*>(vrow") == 1
     assert not verify(list(sched.plan.live_ranges.values()), sched.plan.offsets)
 
 
