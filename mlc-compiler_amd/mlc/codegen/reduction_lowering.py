@@ -36,8 +36,23 @@ class ReductionLoweringError(Exception):
 
 
 def _row_constant_layout(v: Value, frame: Frame) -> Layout:
-    """A row-shaped value with the reduced dims appended at stride 0."""
-    lay = v.layout if tuple(v.shape) == frame.row else v.layout.expand(frame.row)
+    """A row-shaped value with the reduced dims appended at stride 0.
+
+    ``classify`` also places a row-major reshape of the row shape (same
+    element count, e.g. ``[1, 100]`` against row ``(100,)`` when a size-1
+    axis is reduced after a transpose) in the row; that value is read through
+    the reshape. The reference's lowering expands it instead
+    (``reduction_lowering.py:66-68``) and raises a ValueError there."""
+    shape = tuple(v.shape)
+    if shape == frame.row:
+        lay = v.layout
+    elif _broadcasts_to(shape, frame.row):
+        lay = v.layout.expand(frame.row)
+    else:
+        lay = v.layout.reshape(frame.row)
+        if lay is None:
+            raise ReductionLoweringError(
+                f"{v.name} {shape} is neither a broadcast nor a view of the row shape {frame.row}")
     return Layout(frame.row + frame.col, lay.strides + (0,) * len(frame.col), lay.offset)
 
 
@@ -146,6 +161,33 @@ def _held_index(v: Value, frame: Frame) -> IndexMap:
         lay = _row_constant_layout(v, frame)
         axes = [("row", frame.row), ("col", frame.col)]
     return build_index(axes, lay)
+
+
+def reads_held_values(nodes, frame: Frame) -> bool:
+    """True when every member that reads a value another member produces
+    reads it at the index map the kernel holds it at, so ``_Builder.operand``
+    takes it from registers. A read through another map (a permuted view of
+    an in-kernel value, e.g. ``layer_norm(cos(x).transpose(2, 0))``) would
+    become a load of a buffer that this kernel itself writes, or never writes.
+    The reference's fusion groups such a producer and its kernel reads
+    unwritten memory; the fusion pass asks this before merging instead."""
+    produced = {id(o): o for n in nodes for o in n.outputs}
+    for n in nodes:
+        if op_class(n.op) is OpClass.REDUCTION:
+            reads = [(n.args[0], tuple(n.args[0].shape))] if isinstance(n.args[0], Value) else []
+        else:
+            reads = [(a, tuple(n.outputs[0].shape)) for a in n.args if isinstance(a, Value)]
+        for a, target in reads:
+            src = source_value(a)
+            if id(src) not in produced:
+                continue
+            try:
+                axes, lay = frame_layout(a, target, frame)
+                if build_index(axes, lay) != _held_index(src, frame):
+                    return False
+            except (ValueError, ReductionLoweringError):
+                return False
+    return True
 
 
 def build_reduction(graph: Graph, group, stores: set[int], name: str, cfg: Config) -> ReductionKernel:

@@ -8,7 +8,10 @@ column axis.
 
 Reference behaviour followed: ``mlc/passes/reduction_fusion.py:55-379``:
 frame classification, storability, the legality checks and the fixed-point
-growth loop with its neighbour visiting order.
+growth loop with its neighbour visiting order. One check is added: a merge is
+refused when a member would read another member's value through an index map
+other than the one the kernel holds it at (the reference groups such
+producers and its kernel reads memory it never wrote).
 """
 
 from __future__ import annotations
@@ -229,10 +232,19 @@ def fuse_reductions(graph: Graph, gg: GroupGraph, cfg: Config, uses: UseInfo) ->
                 member_ids = {id(n) for n in merged}
                 if not _escape_ok(merged, frame, uses, member_ids):
                     continue
+                if not _reads_held_values(merged, frame):
+                    continue
                 if not _profitable(gg, gi, gj, frame, uses, member_ids, cfg):
                     continue
                 gi = gg.merge(gi, gj)
                 changed = True
+
+
+def _reads_held_values(nodes, frame: Frame) -> bool:
+    # (the lowering owns the frame-to-index-map rules this compares)
+    from ..codegen.reduction_lowering import reads_held_values
+
+    return reads_held_values(nodes, frame)
 
 
 def _neighbours(gg: GroupGraph, gi: int) -> list[int]:

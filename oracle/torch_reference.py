@@ -227,6 +227,15 @@ def run_reduction(k: ReductionKernel, buffers: dict[str, torch.Tensor], chunk: i
             continue
         val = eval_expr(k.out_expr[a.value.name], row_loads, refs,
                         row_loads[0] if row_loads else row)
+        if torch.is_tensor(val) and val.dim() == 2 and val.shape[1] > 1:
+            # A row output does not vary along the row, so every column holds
+            # its value; keep one. The reference's Triton kernels compute it
+            # once per row from scalar loads (triton_reduction.py:94-111,
+            # 268-270); its torch backend stores the full-row value here
+            # (torch_backend.py:182,239-247) and fails with a shape error
+            # when the row output reads a row-constant operand or a bind
+            # evaluated over the row (``x.sum(0, keepdim=True) + y``).
+            val = val[:, :1]
         dest = buffers[a.value.buffer.name]
         off = _offsets(a.index.render(), {"row": row, "col": col0}, row)
         if not torch.is_tensor(val):

@@ -1,0 +1,264 @@
+"""Seeded random programs for parity: independent chains of pointwise ops,
+views (permute, transpose, strided slices, expand), broadcasting operands,
+casts and reductions, all in one module so one compile covers them.
+
+Each chain starts from its own input and draws its ops from what the lowering
+registers (``mlc/ir/ops.py``), so every program compiles; the shapes are
+small and ragged (sizes that 8-element packs do not divide, size-1 dims,
+inner dims that are not the unit-stride one) to reach the kernels' tail,
+strided and gather paths and the transpose template.
+"""
+
+from __future__ import annotations
+
+import random
+
+import torch
+import torch.nn.functional as F
+
+SIZES = (1, 2, 3, 5, 7, 8, 9, 16, 24, 33, 64, 100, 128)
+DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+#: max |got - want| / max(|want|) between the HIP path and the oracle, by the
+#: narrowest dtype a chain stores: a few units in the last place of the narrow
+#: types (a transcendental or summation-order difference can flip one
+#: rounding, which later ops carry), the fp32 bar otherwise
+TOLERANCE = {torch.float32: 1e-5, torch.float16: 4e-3, torch.bfloat16: 3e-2}
+
+
+def _shape(rng: random.Random) -> list[int]:
+    rank = rng.randint(1, 4)
+    while True:
+        s = [rng.choice(SIZES) for _ in range(rank)]
+        n = 1
+        for d in s:
+            n *= d
+        if 16 <= n <= 40000:
+            return s
+
+
+_UNARY = [
+    ("exp", lambda t: torch.exp(torch.tanh(t))),
+    ("tanh", torch.tanh),
+    ("sigmoid", torch.sigmoid),
+    ("relu", torch.relu),
+    ("abs", torch.abs),
+    ("neg", torch.neg),
+    ("sin", torch.sin),
+    ("cos", torch.cos),
+    ("sqrt", lambda t: torch.sqrt(t.abs() + 1.0)),
+    ("rsqrt", lambda t: torch.rsqrt(t.abs() + 0.5)),
+    ("log", lambda t: torch.log(t.abs() + 1.0)),
+    ("gelu", F.gelu),
+    ("gelu_tanh", lambda t: F.gelu(t, approximate="tanh")),
+    ("silu", F.silu),
+    ("square", lambda t: torch.clamp(t, -8.0, 8.0) * torch.clamp(t, -8.0, 8.0)),
+    ("cube", lambda t: torch.pow(torch.clamp(t, -2.0, 2.0), 3)),
+    ("clamp", lambda t: torch.clamp(t, -0.5, 0.7)),
+    ("affine", lambda t: t * 1.7 - 0.3),
+    ("leaky", lambda t: torch.where(t > 0, t, t * 0.1)),
+    ("recip", lambda t: 1.0 / (t.abs() + 1.0)),
+]
+# only as a chain's first op, on the inputs both sides read bit for bit: a
+# floor of a computed value near an integer would turn one ulp into one unit
+_FIRST = [("floor", lambda t: torch.floor(t * 4.0))]
+
+_BINARY = [
+    ("add", torch.add),
+    ("sub", torch.sub),
+    ("mul", lambda a, b: a * torch.tanh(b)),
+    ("max", torch.maximum),
+    ("min", torch.minimum),
+    ("div", lambda a, b: a / (b.abs() + 1.0)),
+    # continuous in its operands: a comparison whose branches differ would
+    # turn a last-place rounding difference into a different value
+    ("where", lambda a, b: torch.where(a > b, a, b)),
+]
+
+
+def _right_aligns(shape: list[int], to: list[int]) -> bool:
+    try:
+        return list(torch.broadcast_shapes(tuple(shape), tuple(to))) == list(to)
+    except RuntimeError:
+        return False
+
+
+class Chain:
+    """One chain: a start shape and dtype, its ops, and the shapes of the
+    extra operands its binary ops read."""
+
+    def __init__(self, rng: random.Random):
+        self.shape = _shape(rng)
+        self.dtype = rng.choice(DTYPES)
+        self.ops: list[tuple] = []
+        self.extra: list[tuple[list[int], torch.dtype]] = []
+        cur = list(self.shape)
+        dtype = self.dtype
+        #: every dtype a value of the chain is stored in
+        self.dtypes = {dtype}
+        reduced = False
+        for step in range(rng.randint(2, 6)):
+            kind = rng.random()
+            if kind < 0.35:
+                name, fn = rng.choice(_UNARY + (_FIRST if step == 0 else []))
+                self.ops.append(("unary", name, fn))
+            elif kind < 0.55:
+                name, fn = rng.choice(_BINARY)
+                # a broadcasting operand: some dims collapsed to 1, maybe fewer dims
+                shp = [d if rng.random() < 0.6 else 1 for d in cur]
+                while len(shp) > 1 and rng.random() < 0.3 and shp[0] == 1:
+                    shp = shp[1:]
+                self.extra.append((shp, dtype))
+                self.ops.append(("binary", name, fn, len(self.extra) - 1))
+            elif kind < 0.75 and len(cur) >= 2:
+                v = rng.choice(["permute", "transpose", "slice", "expand"])
+                if v == "permute":
+                    dims = list(range(len(cur)))
+                    rng.shuffle(dims)
+                    self.ops.append(("view", "permute", dims))
+                    cur = [cur[d] for d in dims]
+                elif v == "transpose":
+                    a, b = rng.sample(range(len(cur)), 2)
+                    self.ops.append(("view", "transpose", (a, b)))
+                    cur[a], cur[b] = cur[b], cur[a]
+                elif v == "slice":
+                    d = rng.randrange(len(cur))
+                    if cur[d] >= 3:
+                        start = rng.randint(0, 1)
+                        stride = rng.choice([1, 2])
+                        self.ops.append(("view", "slice", (d, start, stride)))
+                        cur[d] = len(range(start, cur[d], stride))
+                else:
+                    ones = [i for i, n in enumerate(cur) if n == 1]
+                    if ones:
+                        d = rng.choice(ones)
+                        cur[d] = rng.choice([3, 8])
+                        self.ops.append(("view", "expand", list(cur)))
+            elif kind < 0.83:
+                to = rng.choice([t for t in DTYPES if t != dtype])
+                self.ops.append(("cast", to))
+                dtype = to
+                self.dtypes.add(to)
+            elif not reduced:
+                d = rng.randrange(len(cur))
+                r = rng.choice(["sum", "amax", "mean", "var", "softmax", "layer_norm"])
+                if r == "layer_norm":
+                    d = len(cur) - 1
+                # a normalisation over a few near-equal values turns one ulp
+                # into a unit: keep those rows wide
+                if (r == "layer_norm" and cur[d] < 16) or (r == "var" and cur[d] < 4):
+                    r = "sum"
+                keep = rng.random() < 0.5
+                dropped = cur[:d] + cur[d + 1:]
+                if dropped and _right_aligns(dropped, cur):
+                    # [3, 3, 9] summed over dim 1 gives [3, 9], which also
+                    # right-aligns onto [3, 3, 9]: the reference's frame
+                    # classification reads such a result as varying along the
+                    # reduced axis and refuses the group
+                    # (reduction_fusion.py:136-159, reduction_lowering.py:242)
+                    keep = True
+                self.ops.append(("reduce", r, d, keep))
+                if r not in ("softmax", "layer_norm"):
+                    reduced = True
+                    if keep:
+                        cur[d] = 1
+                    elif len(cur) > 1:
+                        cur.pop(d)
+                    else:
+                        cur = [1]
+                        self.ops[-1] = ("reduce", r, d, True)
+        if not self.ops or self.ops[-1][0] == "view":
+            self.ops.append(("unary", "affine", _UNARY[17][1]))
+
+    def run(self, x, extras):
+        t = x
+        for op in self.ops:
+            kind = op[0]
+            if kind == "unary":
+                t = op[2](t)
+            elif kind == "binary":
+                t = op[2](t, extras[op[3]])
+            elif kind == "view":
+                if op[1] == "permute":
+                    t = t.permute(*op[2])
+                elif op[1] == "transpose":
+                    t = t.transpose(*op[2])
+                elif op[1] == "slice":
+                    d, start, step = op[2]
+                    t = t[(slice(None),) * d + (slice(start, None, step),)]
+                else:
+                    t = t.expand(*op[2])
+            elif kind == "cast":
+                t = t.to(op[1])
+            else:
+                _, r, d, keep = op
+                if r == "sum":
+                    t = t.sum(dim=d, keepdim=keep)
+                elif r == "amax":
+                    t = t.amax(dim=d, keepdim=keep)
+                elif r == "mean":
+                    t = t.mean(dim=d, keepdim=keep)
+                elif r == "var":
+                    t = t.var(dim=d, keepdim=keep, unbiased=False)
+                elif r == "softmax":
+                    t = t.softmax(dim=d)
+                else:
+                    t = F.layer_norm(t, (t.shape[-1],))
+        return t
+
+
+class Program(torch.nn.Module):
+    """``n`` independent chains; forward takes every chain's inputs in order
+    and returns one output per chain."""
+
+    def __init__(self, seed: int, n: int):
+        super().__init__()
+        rng = random.Random(seed)
+        self.chains = [Chain(rng) for _ in range(n)]
+
+    def forward(self, *args):
+        outs = []
+        i = 0
+        for c in self.chains:
+            x = args[i]
+            extras = args[i + 1:i + 1 + len(c.extra)]
+            i += 1 + len(c.extra)
+            outs.append(c.run(x, extras))
+        return tuple(outs)
+
+
+def tolerance(chain: Chain) -> float:
+    """The bar for ``chain`` against the oracle: set by the narrowest dtype
+    any of its values is stored in."""
+    return max(TOLERANCE[d] for d in chain.dtypes)
+
+
+def program(seed: int, n: int = 24):
+    """(model, example inputs) for ``seed``: values N(0, 1) from a generator
+    seeded with ``seed``."""
+    model = Program(seed, n)
+    g = torch.Generator().manual_seed(seed)
+    args = []
+    for c in model.chains:
+        args.append(torch.randn(c.shape, generator=g).to(c.dtype))
+        for shp, dt in c.extra:
+            args.append(torch.randn(shp, generator=g).to(dt))
+    return model, tuple(args)
+
+
+def max_rel_error(got: torch.Tensor, want: torch.Tensor) -> float:
+    g, w = got.double(), want.double()
+    if w.numel() == 0:
+        return 0.0
+    both_nan = torch.isnan(g) & torch.isnan(w)
+    if not torch.equal(torch.isnan(g), torch.isnan(w)):
+        return float("inf")
+    g, w = g[~both_nan], w[~both_nan]
+    inf = torch.isinf(w)
+    if not torch.equal(g[inf], w[inf]):
+        return float("inf")
+    g, w = g[~inf], w[~inf]
+    if w.numel() == 0:
+        return 0.0
+    scale = max(w.abs().max().item(), 1e-3)
+    return (g - w).abs().max().item() / scale

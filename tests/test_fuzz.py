@@ -1,0 +1,147 @@
+"""Seeded random programs (``fuzz_programs``) and the front-end edge cases
+they found, pinned against the reference's own behaviour on them
+(``golden/reference_edge_cases.json``).
+
+CPU: every random chain through the oracle against eager PyTorch, and each
+edge case against the fixture. GPU: the same random programs through the HIP
+path against the oracle, under the default passes, streamed reductions and
+layout selection.
+"""
+
+from __future__ import annotations
+
+import json
+import pathlib
+
+import pytest
+import torch
+
+import fuzz_programs as fp
+from golden.dump_edge_cases import cases
+from mlc.api import build_pipeline
+from mlc.codegen.reduction_lowering import ReductionLoweringError
+from mlc.config import Config
+from mlc.ir.capture import capture
+from oracle import compile_reference
+
+FIXTURE = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_edge_cases.json")
+                     .read_text())["cases"]
+CFG = Config(cuda_graphs=False)
+
+
+def _tuple(out):
+    return tuple(out) if isinstance(out, (list, tuple)) else (out,)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_programs_oracle_matches_eager(seed):
+    """Every chain compiles, and the oracle agrees with eager PyTorch: at the
+    fp32 bar for all-fp32 chains; within 2e-2 (fp16) / 6e-2 (bf16) of the
+    largest output where a value is stored narrow, since a fused kernel keeps
+    fp32 between its loads and stores and eager rounds after every op."""
+    model, args = fp.program(seed)
+    got = _tuple(compile_reference(model, args, CFG)(*args))
+    with torch.no_grad():
+        want = model(*args)
+    assert len(got) == len(want) == len(model.chains)
+    for c, g, w in zip(model.chains, got, want):
+        assert g.shape == w.shape and g.dtype == w.dtype
+        bar = 6e-2 if torch.bfloat16 in c.dtypes else 2e-2 if torch.float16 in c.dtypes else 1e-5
+        assert fp.max_rel_error(g, w) <= bar, (c.shape, c.dtype, [o[:2] for o in c.ops])
+
+
+def _case(name):
+    return next((m, a) for n, m, a in cases() if n == name)
+
+
+def test_edge_case_reference_errors_are_kept():
+    """A keepdim=False result whose shape right-aligns onto the element shape
+    is refused with the reference's error and message."""
+    model, args = _case("right_aligned_row_result")
+    kind, msg = FIXTURE["right_aligned_row_result"]["error"]
+    with pytest.raises(ReductionLoweringError) as e:
+        build_pipeline(capture(model, args), CFG)
+    assert kind == "ReductionLoweringError" and str(e.value) == msg
+
+
+def test_edge_case_row_output_reading_an_operand():
+    """Same schedule as the reference (kernel summaries and index strings);
+    the reference's torch backend fails on it (recorded), the oracle stores
+    the row value its Triton kernels compute."""
+    model, args = _case("row_output_reads_operand")
+    rec = FIXTURE["row_output_reads_operand"]
+    assert rec["run_error"][0] == "AttributeError"
+    sched = build_pipeline(capture(model, args), CFG)
+    assert [k.summary() for k in sched.kernels] == [k["summary"] for k in rec["kernels"]]
+    assert [[[a.value.buffer.name, a.index.render()] for a in k.inputs] for k in sched.kernels] \
+        == [k["inputs"] for k in rec["kernels"]]
+    got = compile_reference(model, args, CFG)(*args)
+    torch.testing.assert_close(got, model(*args), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("name", ["reshaped_row_operand", "permuted_row_value"])
+def test_edge_cases_the_reference_cannot_lower(name):
+    """The reference raises ValueError while lowering these (recorded); here
+    they compile and match eager."""
+    model, args = _case(name)
+    assert FIXTURE[name]["error"][0] == "ValueError"
+    got = compile_reference(model, args, CFG)(*args)
+    with torch.no_grad():
+        want = model(*args)
+    assert fp.max_rel_error(got, want) <= 2e-2
+
+
+def test_edge_case_permuted_producer_is_not_fused():
+    """The reference fuses ``cos`` into the LayerNorm over its transposed
+    view and reads a buffer its kernel never writes (non-finite output,
+    recorded). Here the merge is refused: ``cos`` is its own kernel and the
+    result matches eager."""
+    model, args = _case("permuted_element_producer")
+    rec = FIXTURE["permuted_element_producer"]
+    assert rec["finite"] is False and rec["matches_eager"] is False
+    assert "cos" in rec["kernels"][0]["summary"] and len(rec["kernels"]) == 1
+    sched = build_pipeline(capture(model, args), CFG)
+    assert [k.summary().split(": ", 1)[1].split(" ")[0] for k in sched.kernels] == \
+        ["pointwise[7,", "reduction"]
+    got = compile_reference(model, args, CFG)(*args)
+    torch.testing.assert_close(got, model(*args), rtol=1e-5, atol=1e-5)
+
+
+GPU_CASES = [(s, "default") for s in range(16)] + [(s, "streamed") for s in range(6)] + \
+    [(s, "layout") for s in range(4)]
+GPU_CONFIGS = {"default": CFG, "streamed": Config(cuda_graphs=False, max_persistent_row=16),
+               "layout": Config(cuda_graphs=False, layout_selection=True)}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed,cname", GPU_CASES)
+def test_random_programs_hip_matches_oracle(seed, cname):
+    """The HIP path against the oracle on the same inputs, chain by chain, at
+    the bar of the narrowest dtype each chain stores (``fp.TOLERANCE``)."""
+    import mlc
+
+    cfg = GPU_CONFIGS[cname]
+    model, args = fp.program(seed)
+    want = _tuple(compile_reference(model, args, cfg)(*args))
+    dev = tuple(a.cuda() for a in args)
+    print(f"seed {seed} {cname}: {len(model.chains)} chains", flush=True)
+    got = _tuple(mlc.compile(model, dev, cfg)(*dev))
+    torch.cuda.synchronize()
+    for c, g, w in zip(model.chains, got, want):
+        assert g.shape == w.shape and g.dtype == w.dtype
+        err = fp.max_rel_error(g.cpu(), w)
+        assert err <= fp.tolerance(c), (err, c.shape, c.dtype, [o[:2] for o in c.ops])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["row_output_reads_operand", "reshaped_row_operand",
+                                  "permuted_element_producer", "permuted_row_value"])
+def test_edge_cases_hip_matches_oracle(name):
+    import mlc
+
+    model, args = _case(name)
+    want = compile_reference(model, args, CFG)(*args)
+    dev = tuple(a.cuda() for a in args)
+    got = mlc.compile(model, dev, CFG)(*dev)
+    torch.cuda.synchronize()
+    assert fp.max_rel_error(got.cpu(), want) <= fp.TOLERANCE[want.dtype]
