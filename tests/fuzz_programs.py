@@ -26,14 +26,20 @@ DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 TOLERANCE = {torch.float32: 1e-5, torch.float16: 4e-3, torch.bfloat16: 3e-2}
 
 
-def _shape(rng: random.Random) -> list[int]:
-    rank = rng.randint(1, 4)
+#: row lengths beyond one wave's reach (multi-wave rows, long streamed rows)
+WIDE = (700, 1000, 2049, 4099)
+
+
+def _shape(rng: random.Random, wide: bool = False) -> list[int]:
+    rank = rng.randint(1, 4 if not wide else 3)
     while True:
         s = [rng.choice(SIZES) for _ in range(rank)]
+        if wide:
+            s[rng.randrange(rank)] = rng.choice(WIDE)
         n = 1
         for d in s:
             n *= d
-        if 16 <= n <= 40000:
+        if 16 <= n <= (40000 if not wide else 200000):
             return s
 
 
@@ -60,8 +66,19 @@ _UNARY = [
     ("recip", lambda t: 1.0 / (t.abs() + 1.0)),
 ]
 # only as a chain's first op, on the inputs both sides read bit for bit: a
-# floor of a computed value near an integer would turn one ulp into one unit
+# floor or integer conversion of a computed value near an integer would turn
+# one ulp into one unit
 _FIRST = [("floor", lambda t: torch.floor(t * 4.0))]
+_TO_INT = ("to_int", lambda t: (t * 4.0).to(torch.int64))
+_INT_OPS = [
+    ("int_affine", lambda t: t * 3 - 2),
+    ("int_abs", torch.abs),
+    ("int_neg", torch.neg),
+    ("int_max", lambda t: torch.maximum(t, torch.zeros_like(t))),
+    ("int_mask", lambda t: torch.where(t > 1, t, t - 5)),
+    ("int_bool", lambda t: torch.logical_and(t > 0, t < 3)),
+    ("int_to_float", lambda t: t.to(torch.float32) * 0.25),
+]
 
 _BINARY = [
     ("add", torch.add),
@@ -87,8 +104,8 @@ class Chain:
     """One chain: a start shape and dtype, its ops, and the shapes of the
     extra operands its binary ops read."""
 
-    def __init__(self, rng: random.Random):
-        self.shape = _shape(rng)
+    def __init__(self, rng: random.Random, wide: bool = False):
+        self.shape = _shape(rng, wide)
         self.dtype = rng.choice(DTYPES)
         self.ops: list[tuple] = []
         self.extra: list[tuple[list[int], torch.dtype]] = []
@@ -97,10 +114,22 @@ class Chain:
         #: every dtype a value of the chain is stored in
         self.dtypes = {dtype}
         reduced = False
+        if rng.random() < 0.15:
+            # an integer prefix: int64 arithmetic, comparisons to bool, back to fp32
+            self.ops.append(("unary",) + _TO_INT)
+            for _ in range(rng.randint(1, 3)):
+                name, fn = rng.choice(_INT_OPS[:5])
+                self.ops.append(("unary", name, fn))
+            name, fn = rng.choice(_INT_OPS[5:])
+            self.ops.append(("unary", name, fn))
+            if name == "int_bool":
+                self.ops.append(("unary", "bool_to_float", lambda t: t.to(torch.float32) - 0.5))
+            dtype = torch.float32
+            self.dtypes.add(dtype)
         for step in range(rng.randint(2, 6)):
             kind = rng.random()
             if kind < 0.35:
-                name, fn = rng.choice(_UNARY + (_FIRST if step == 0 else []))
+                name, fn = rng.choice(_UNARY + (_FIRST if not self.ops else []))
                 self.ops.append(("unary", name, fn))
             elif kind < 0.55:
                 name, fn = rng.choice(_BINARY)
@@ -211,10 +240,10 @@ class Program(torch.nn.Module):
     """``n`` independent chains; forward takes every chain's inputs in order
     and returns one output per chain."""
 
-    def __init__(self, seed: int, n: int):
+    def __init__(self, seed: int, n: int, wide: bool = False):
         super().__init__()
         rng = random.Random(seed)
-        self.chains = [Chain(rng) for _ in range(n)]
+        self.chains = [Chain(rng, wide) for _ in range(n)]
 
     def forward(self, *args):
         outs = []
@@ -233,10 +262,10 @@ def tolerance(chain: Chain) -> float:
     return max(TOLERANCE[d] for d in chain.dtypes)
 
 
-def program(seed: int, n: int = 24):
+def program(seed: int, n: int = 24, wide: bool = False):
     """(model, example inputs) for ``seed``: values N(0, 1) from a generator
-    seeded with ``seed``."""
-    model = Program(seed, n)
+    seeded with ``seed``. ``wide`` gives every chain one dim of 700..4099."""
+    model = Program(seed, n, wide)
     g = torch.Generator().manual_seed(seed)
     args = []
     for c in model.chains:

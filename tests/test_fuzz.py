@@ -5,7 +5,8 @@ they found, pinned against the reference's own behaviour on them
 CPU: every random chain through the oracle against eager PyTorch, and each
 edge case against the fixture. GPU: the same random programs through the HIP
 path against the oracle, under the default passes, streamed reductions and
-layout selection.
+layout selection, and programs with rows of 700..4099 (rows spread over
+several waves, persistent and streamed).
 """
 
 from __future__ import annotations
@@ -33,13 +34,13 @@ def _tuple(out):
     return tuple(out) if isinstance(out, (list, tuple)) else (out,)
 
 
-@pytest.mark.parametrize("seed", range(6))
-def test_random_programs_oracle_matches_eager(seed):
+@pytest.mark.parametrize("seed,wide", [(s, False) for s in range(6)] + [(s, True) for s in range(2)])
+def test_random_programs_oracle_matches_eager(seed, wide):
     """Every chain compiles, and the oracle agrees with eager PyTorch: at the
     fp32 bar for all-fp32 chains; within 2e-2 (fp16) / 6e-2 (bf16) of the
     largest output where a value is stored narrow, since a fused kernel keeps
     fp32 between its loads and stores and eager rounds after every op."""
-    model, args = fp.program(seed)
+    model, args = fp.program(seed, wide=wide)
     got = _tuple(compile_reference(model, args, CFG)(*args))
     with torch.no_grad():
         want = model(*args)
@@ -108,9 +109,11 @@ def test_edge_case_permuted_producer_is_not_fused():
 
 
 GPU_CASES = [(s, "default") for s in range(16)] + [(s, "streamed") for s in range(6)] + \
-    [(s, "layout") for s in range(4)]
+    [(s, "layout") for s in range(4)] + [(s, "wide") for s in range(6)] + \
+    [(s, "wide_streamed") for s in range(3)]
 GPU_CONFIGS = {"default": CFG, "streamed": Config(cuda_graphs=False, max_persistent_row=16),
-               "layout": Config(cuda_graphs=False, layout_selection=True)}
+               "layout": Config(cuda_graphs=False, layout_selection=True), "wide": CFG,
+               "wide_streamed": Config(cuda_graphs=False, max_persistent_row=512)}
 
 
 @pytest.mark.gpu
@@ -121,7 +124,7 @@ def test_random_programs_hip_matches_oracle(seed, cname):
     import mlc
 
     cfg = GPU_CONFIGS[cname]
-    model, args = fp.program(seed)
+    model, args = fp.program(seed, wide=cname.startswith("wide"))
     want = _tuple(compile_reference(model, args, cfg)(*args))
     dev = tuple(a.cuda() for a in args)
     print(f"seed {seed} {cname}: {len(model.chains)} chains", flush=True)
