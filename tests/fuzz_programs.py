@@ -291,3 +291,46 @@ def max_rel_error(got: torch.Tensor, want: torch.Tensor) -> float:
         return 0.0
     scale = max(w.abs().max().item(), 1e-3)
     return (g - w).abs().max().item() / scale
+
+
+def attention_case(seed: int):
+    """A random attention problem for the fused kernels: (model, inputs,
+    description). Queries in multiples of 16; up to 128 keys in multiples of
+    32 (single pass) or 192..640 in multiples of 64 (key-blocked); head sizes
+    32..128; one of five masks: padding at -10000 or -inf, causal (-inf, every
+    row keeps its diagonal), a per-head additive bias, or zeros. Scaled by a
+    division or a multiplication."""
+    import math
+
+    rng = random.Random(1000 + seed)
+    b, h = rng.choice([1, 2, 3]), rng.choice([1, 2, 4, 12])
+    t = 16 * rng.randint(1, 16)
+    tk = 32 * rng.randint(1, 4) if rng.random() < 0.5 else 64 * rng.randint(3, 10)
+    d = rng.choice([32, 64, 96, 128])
+    kind = rng.choice(["padding", "padding_inf", "causal", "bias", "zeros"])
+    by_div = rng.random() < 0.5
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, h, t, d, generator=g).half()
+    k = torch.randn(b, h, tk, d, generator=g).half()
+    v = torch.randn(b, h, tk, d, generator=g).half()
+    if kind in ("padding", "padding_inf"):
+        keep = torch.rand(b, 1, 1, tk, generator=g) >= 0.2
+        keep[..., 0] = True
+        fill = -10000.0 if kind == "padding" else float("-inf")
+        mask = torch.where(keep, 0.0, fill).half()
+    elif kind == "causal":
+        mask = torch.triu(torch.full((t, tk), float("-inf")), diagonal=1 + max(0, tk - t))
+        mask = mask.half()[None, None]
+    elif kind == "bias":
+        mask = torch.randn(1, h, t, tk, generator=g).half()
+    else:
+        mask = torch.zeros(b, 1, 1, tk).half()
+
+    class Attn(torch.nn.Module):
+        def forward(self, q, k, v, mask):
+            s = q @ k.transpose(-2, -1)
+            s = s / math.sqrt(d) if by_div else s * (1.0 / math.sqrt(d))
+            return (s + mask).softmax(dim=-1) @ v
+
+    desc = f"b{b} h{h} T{t} Tk{tk} d{d} {kind} {'div' if by_div else 'mul'}"
+    return Attn(), (q, k, v, mask), desc

@@ -148,3 +148,45 @@ def test_edge_cases_hip_matches_oracle(name):
     got = mlc.compile(model, dev, CFG)(*dev)
     torch.cuda.synchronize()
     assert fp.max_rel_error(got.cpu(), want) <= fp.TOLERANCE[want.dtype]
+
+
+ATTN = Config(fused_attention=True, cuda_graphs=False)
+
+
+def _fp64_err(got, model, args):
+    exact = model(*(a.double() for a in args))
+    return ((got.double().cpu() - exact).abs().max() / exact.abs().max()).item()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_attention_oracle_matches_float64(seed):
+    """Random attention problems fuse into one attention kernel, and the
+    oracle's fused kernel is within 2e-3 of float64 attention."""
+    from mlc.kernels import AttentionKernel
+
+    model, args, desc = fp.attention_case(seed)
+    sched = build_pipeline(capture(model, args), ATTN)
+    assert sum(isinstance(k, AttentionKernel) for k in sched.kernels) == 1, desc
+    got = compile_reference(model, args, ATTN)(*args)
+    assert torch.isfinite(got).all() and _fp64_err(got, model, args) <= 2e-3, desc
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(24))
+def test_random_attention_hip_matches_oracle(seed):
+    """The MFMA attention kernels (single pass and key-blocked) on random
+    problems: within 2e-3 of the oracle's fused kernel and of float64."""
+    import mlc
+
+    model, args, desc = fp.attention_case(seed)
+    want = compile_reference(model, args, ATTN)(*args)
+    dev = tuple(a.cuda() for a in args)
+    print(desc, flush=True)
+    compiled = mlc.compile(model, dev, ATTN)
+    assert [s.meta["kind"] for s in compiled._module.launch_table.values()].count("attention") == 1
+    got = compiled(*dev)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all(), desc
+    e_oracle, e_exact = fp.max_rel_error(got.cpu(), want), _fp64_err(got, model, args)
+    print(f"  hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}", flush=True)
+    assert e_oracle <= 2e-3 and e_exact <= 2e-3, desc
