@@ -38,7 +38,7 @@ reduction kernel, and the softmax's exp and division take fast forms
 from __future__ import annotations
 
 from ..kernels import AttentionKernel, Bind
-from .hip_backend import (_IDENTITY, _OP, WAVE, LaunchSpec, Renderer, _RowOffsets,
+from .hip_backend import (_IDENTITY, _OP, STORAGE, WAVE, LaunchSpec, Renderer, _RowOffsets,
                           _expr_varies, _params, _reciprocal_divisors, _reciprocal_lines,
                           _row_col_access, _scalar_division, axis_terms, cast_code,
                           compute_type, index_type, join_offset, render_terms)
@@ -549,6 +549,36 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
             L.append(f"  const {t} {nm} = {code};")
     exp_ = "mlc::exp_fast" if FAST_SOFTMAX_MATH else "mlc::exp_"
 
+    mask_slots = [i for i in col_slots if i != k.score_slot]
+
+    def mask_loads(kc: str, ind: str) -> list[str]:
+        out = []
+        for i in mask_slots:
+            a = sm.inputs[i]
+            acc = _row_col_access(sm, a, 4)
+            p = param[i]
+            out.append(f"{ind}{{ const {it} rb = {offs.row(a)};")
+            out.append("#pragma unroll")
+            out.append(f"{ind}  for (int t = 0; t < {NT}; ++t) {{")
+            out.append(f"{ind}    const {it} c0 = ({it})({kc} + t * 16 + g * 4);")
+            if acc.mode == "affine" and acc.aligned:
+                out.append(f"{ind}    xr{i}[t] = *reinterpret_cast<const mlc::pack<{STORAGE[a.dtype]}, 4>*>"
+                           f"(in{p} + rb + {offs.col(a, 'c0')});")
+            else:
+                out.append("#pragma unroll")
+                out.append(f"{ind}    for (int j = 0; j < 4; ++j) xr{i}[t].x[j] = "
+                           f"in{p}[rb + {offs.col(a, '(c0 + (' + it + ')j)')}];")
+            out.append(f"{ind}  }}")
+            out.append(f"{ind}}}")
+        return out
+
+    for i in mask_slots:
+        L.append(f"  mlc::pack<{STORAGE[sm.inputs[i].dtype]}, 4> xr{i}[{NT}];")
+    if mask_slots:
+        L.append("  if (active) {")
+        L += mask_loads("0", "    ")
+        L.append("  }")
+
     L.append(f"  for (int b = 0; b < {NB}; ++b) {{")
     L.append(f"    if (b + 1 < {NB}) {{  // next block's loads, in flight during this block's math")
     L.append(f"      kb0 = (b + 1) * {KB};")
@@ -556,35 +586,37 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("    }")
     L.append("    if (active) {")
     L.append(f"      const int kc = b * {KB};")
+    # every tile's operands of one head-dim chunk are read before its MFMAs,
+    # and the tiles' four accumulations are independent: LDS and MFMA latency
+    # overlap instead of alternating (each tile still sums its chunks in order)
+    L.append(f"      mlc::float4v acc[{NT}];")
+    L.append("#pragma unroll")
+    L.append(f"      for (int t = 0; t < {NT}; ++t) acc[t] = mlc::float4v{{0.0f, 0.0f, 0.0f, 0.0f}};")
+    L.append("#pragma unroll")
+    L.append(f"      for (int dc = 0; dc < {D // 32}; ++dc) {{")
+    L.append(f"        mlc::half8 kf[{NT}];")
+    L.append("#pragma unroll")
+    L.append(f"        for (int t = 0; t < {NT}; ++t) kf[t] = *reinterpret_cast<const mlc::half8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
+    L.append("#pragma unroll")
+    L.append(f"        for (int t = 0; t < {NT}; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t], qf[dc], acc[t], 0, 0, 0);")
+    L.append("      }")
     L.append(f"      float s[{NT}][4];")
     L.append("#pragma unroll")
-    L.append(f"      for (int t = 0; t < {NT}; ++t) {{")
-    L.append("        mlc::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};")
+    L.append(f"      for (int t = 0; t < {NT}; ++t)")
     L.append("#pragma unroll")
-    L.append(f"        for (int dc = 0; dc < {D // 32}; ++dc) {{")
-    L.append(f"          const mlc::half8 kf = *reinterpret_cast<const mlc::half8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
-    L.append("          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[dc], acc, 0, 0, 0);")
-    L.append("        }")
-    L.append("#pragma unroll")
-    L.append(f"        for (int i = 0; i < 4; ++i) s[t][i] = {cast_code('acc[i]', k.score_dtype)[0]};")
-    L.append("      }")
-    for i, a in enumerate(sm.inputs):
-        if i == k.score_slot or i not in col_slots:
-            continue
-        acc = _row_col_access(sm, a, 4)
-        p = param[i]
+    L.append(f"        for (int i = 0; i < 4; ++i) s[t][i] = {cast_code('acc[t][i]', k.score_dtype)[0]};")
+    # the other column operands (the mask): widened from the words loaded one
+    # block ahead, then the next block's words are requested, so their memory
+    # latency overlaps this block's work as the K/V tiles' does
+    for i in mask_slots:
         L.append(f"      {in_types[i]} x{i}[{NT}][4];")
-        L.append(f"      {{ const {it} rb = {offs.row(a)};")
         L.append("#pragma unroll")
-        L.append(f"        for (int t = 0; t < {NT}; ++t) {{")
-        L.append(f"          const {it} c0 = ({it})(kc + t * 16 + g * 4);")
-        if acc.mode == "affine" and acc.aligned:
-            L.append(f"          mlc::load_pack<4>(x{i}[t], in{p} + rb + {offs.col(a, 'c0')});")
-        else:
-            L.append("#pragma unroll")
-            L.append(f"          for (int j = 0; j < 4; ++j) x{i}[t][j] = "
-                     f"mlc::ld(in{p} + rb + {offs.col(a, '(c0 + (' + it + ')j)')});")
-        L.append("        }")
+        L.append(f"      for (int t = 0; t < {NT}; ++t)")
+        L.append("#pragma unroll")
+        L.append(f"        for (int j = 0; j < 4; ++j) x{i}[t][j] = mlc::ld(&xr{i}[t].x[j]);")
+    if mask_slots:
+        L.append(f"      if (b + 1 < {NB}) {{")
+        L += mask_loads("(kc + " + str(KB) + ")", "        ")
         L.append("      }")
     for nm in [s.name for s in sm.steps if s.name in needed]:
         st = by_name[nm]
@@ -611,6 +643,15 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("      // a block whose scores are all -inf for every row of the wave (a causal")
     L.append("      // mask's upper triangle) adds exactly nothing: skip its exp and P.V")
     L.append("      if (!__all(mb == (-__builtin_huge_valf()))) {")
+    if D <= 64:
+        # the V^T operands do not depend on the probabilities: read them now,
+        # so their LDS latency hides behind the exponentials
+        L.append(f"      mlc::half8 va[{D // 16}][{NT // 2}];")
+        L.append("#pragma unroll")
+        L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt)")
+        L.append("#pragma unroll")
+        L.append(f"        for (int m = 0; m < {NT // 2}; ++m)")
+        L.append(f"          va[dt][m] = *reinterpret_cast<const mlc::half8*>(vt + (dt * 16 + ql) * {PV} + g * 8 + m * 32);  // keys vperm-ed")
     L.append("      const float m_new = mlc::max_<float>(m_run, mb);")
     L.append(f"      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : {exp_}(m_run - m_new);")
     L.append("      // a row with no finite score yet subtracts 0: its x are all -inf, exp gives 0")
@@ -627,18 +668,31 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("        }")
     L.append("      l_run = l_run * alpha + psum;")
     L.append("      m_run = m_new;")
+    L.append(f"      mlc::half8 bq[{NT // 2}];")
     L.append("#pragma unroll")
-    L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt) {{")
-    L.append("        o[dt] *= alpha;")
-    L.append(f"        const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
-    L.append("#pragma unroll")
-    L.append(f"        for (int m = 0; m < {NT // 2}; ++m) {{")
-    L.append("          const mlc::half8 a = *reinterpret_cast<const mlc::half8*>(vrow + m * 32);")
-    L.append("          const mlc::half8 bq = {p[2 * m][0], p[2 * m][1], p[2 * m][2], p[2 * m][3], "
+    L.append(f"      for (int m = 0; m < {NT // 2}; ++m)")
+    L.append("        bq[m] = mlc::half8{p[2 * m][0], p[2 * m][1], p[2 * m][2], p[2 * m][3], "
              "p[2 * m + 1][0], p[2 * m + 1][1], p[2 * m + 1][2], p[2 * m + 1][3]};")
-    L.append("          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, o[dt], 0, 0, 0);")
-    L.append("        }")
-    L.append("      }")
+    L.append("#pragma unroll")
+    L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt) o[dt] *= alpha;")
+    if D <= 64:
+        # the head-dim tiles' accumulations are independent; each still sums
+        # its key pairs in order
+        L.append("#pragma unroll")
+        L.append(f"      for (int m = 0; m < {NT // 2}; ++m)")
+        L.append("#pragma unroll")
+        L.append(f"        for (int dt = 0; dt < {D // 16}; ++dt)")
+        L.append("          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt][m], bq[m], o[dt], 0, 0, 0);")
+    else:
+        L.append("#pragma unroll")
+        L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt) {{")
+        L.append(f"        const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
+        L.append("#pragma unroll")
+        L.append(f"        for (int m = 0; m < {NT // 2}; ++m) {{")
+        L.append("          const mlc::half8 a = *reinterpret_cast<const mlc::half8*>(vrow + m * 32);")
+        L.append("          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[m], o[dt], 0, 0, 0);")
+        L.append("        }")
+        L.append("      }")
     L.append("      }")
     L.append("    }")
     L.append("    __syncthreads();  // every wave is done with this block's tiles")

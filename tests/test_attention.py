@@ -213,9 +213,9 @@ def test_context_copy_folds_into_the_attention_stores():
 
 def test_long_rows_use_the_key_blocked_kernel():
     """GPT-2 b32 s512 (512 keys) is key-blocked: 64-key blocks streamed
-    through LDS, next block's loads in flight, one division by the row sum at
-    the end; the scores and probabilities (201 MB each per layer) are gone
-    from the arena."""
+    through LDS, next block's loads (K, V and the mask) in flight, one
+    division by the row sum at the end; the scores and probabilities (201 MB
+    each per layer) are gone from the arena."""
     base = build_pipeline(graph_of("C5"), Config())
     sched = build_pipeline(graph_of("C5"), Config(fused_attention=True))
     mod = generate_module(sched, Config(fused_attention=True))
