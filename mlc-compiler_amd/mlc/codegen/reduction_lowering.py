@@ -25,8 +25,8 @@ from ..ir.scalar import loads as expr_loads
 from ..ir.scalar import substitute
 from ..ir.types import Layout
 from ..kernels import Bind, KernelArg, Reduce, ReductionKernel
-from ..passes.reduction_fusion import (ROW, Frame, _broadcasts_to, _group_frame, classify,
-                                       frame_axes, storable)
+from ..passes.reduction_fusion import (ROW, Frame, _broadcasts_to, _group_frame, classify_value,
+                                       frame_axes, storable_value)
 from ..passes.scheduler import source_value
 from .index import IndexMap, build_index
 
@@ -157,7 +157,8 @@ def _held_index(v: Value, frame: Frame) -> IndexMap:
     """Map a value produced in the kernel is held at (compared against later
     reads to decide register reuse)."""
     axes, lay = frame_layout(v, tuple(v.shape), frame)
-    if classify(v.shape, frame) == ROW and not _broadcasts_to(v.shape, frame.element):
+    if classify_value(v, frame) == ROW and (tuple(v.shape) == frame.row
+                                            or not _broadcasts_to(v.shape, frame.element)):
         lay = _row_constant_layout(v, frame)
         axes = [("row", frame.row), ("col", frame.col)]
     return build_index(axes, lay)
@@ -235,11 +236,11 @@ def build_reduction(graph: Graph, group, stores: set[int], name: str, cfg: Confi
         for o in node.outputs:
             if id(o) not in stores:
                 continue
-            if not storable(o.shape, frame):
+            if not storable_value(o, frame):
                 raise ReductionLoweringError(
                     f"{node.op} result {o.name}{list(o.shape)} is broadcast inside its kernel "
                     "but escapes it; the fusion pass should not have grouped it")
-            if classify(o.shape, frame) == ROW:
+            if classify_value(o, frame) == ROW:
                 imap = build_index([("row", frame.row)], Layout.contiguous(frame.row))
                 row_outputs.add(o.name)
             else:

@@ -144,6 +144,27 @@ def frame_axes(shape: tuple[int, ...], frame: Frame) -> list[tuple[str, tuple[in
     return [("row", frame.row), ("col", frame.col)]
 
 
+def classify_value(v: Value, frame: Frame) -> str | None:
+    """``classify`` for a value of the graph. A reduction's own keepdim=False
+    result is a row value even when its shape also right-aligns onto the
+    element shape (``[1, 128]`` against ``[1, 128, 128]``: LayerNorm with
+    batch 1 and rows as long as the sequence). The reference classifies by
+    shape alone there, so its lowering refuses every graph holding such a
+    reduction (``reduction_lowering.py:242``); nothing it compiles changes."""
+    p = v.producer
+    if (p is not None and op_class(p.op) is OpClass.REDUCTION and tuple(v.shape) == frame.row
+            and frame_of(p) == frame):
+        return ROW
+    return classify(v.shape, frame)
+
+
+def storable_value(v: Value, frame: Frame) -> bool:
+    """``storable`` for a value of the graph (see ``classify_value``)."""
+    if classify_value(v, frame) == ROW:
+        return _prod(v.shape) == frame.n_rows
+    return storable(v.shape, frame)
+
+
 def storable(shape: tuple[int, ...], frame: Frame) -> bool:
     """True when every point of ``shape`` is visited exactly once."""
     where = classify(shape, frame)
@@ -167,7 +188,7 @@ def _members_fit(nodes: Iterable[Node], frame: Frame) -> bool:
         if cls is OpClass.REDUCTION:
             if frame_of(n) != frame or not is_associative(reduce_kind(n)):
                 return False
-            if any(classify(o.shape, frame) != ROW for o in n.outputs):
+            if any(classify_value(o, frame) != ROW for o in n.outputs):
                 return False
             continue
         if cls is not OpClass.POINTWISE:
@@ -180,7 +201,7 @@ def _members_fit(nodes: Iterable[Node], frame: Frame) -> bool:
 def _escape_ok(nodes, frame: Frame, uses: UseInfo, member_ids: set[int]) -> bool:
     for n in nodes:
         for o in n.outputs:
-            if storable(o.shape, frame):
+            if storable_value(o, frame):
                 continue
             if uses.escapes(o) or not uses.consumers(o) <= member_ids:
                 return False

@@ -4,8 +4,9 @@ reference).
 
 Each case is a small program at the edge of the reduction-fusion frame rules:
 a row output that reads a row-constant operand, a reshape of the row shape,
-shapes that right-align onto the element shape, a permutation that passes
-the reshape test. Per case the fixture records what the reference does:
+shapes that right-align onto the element shape (among them a LayerNorm whose
+batch is 1 and whose rows are as long as the sequence), a permutation that
+passes the reshape test. Per case the fixture records what the reference does:
 the exception it raises (type and message), or its schedule (kernel
 summaries, operand buffers and index strings) and whether its torch backend's
 outputs agree with eager PyTorch (or the error its torch backend raises). Nothing else pins the front end there: the
@@ -49,6 +50,10 @@ def cases():
         def forward(self, x, y):
             return torch.sqrt((x.mean(dim=3, keepdim=True) + y).permute(1, 2, 3, 0).abs())
 
+    class LayerNormRowMatchesTrailing(torch.nn.Module):
+        def forward(self, x):
+            return F.layer_norm(x, (x.shape[-1],))
+
     g = torch.Generator().manual_seed(0)
 
     def rn(*s, dt=torch.float32):
@@ -62,6 +67,8 @@ def cases():
          (rn(3, 3, 9, 128, dt=torch.float16), rn(1, 1, 1, dt=torch.float16))),
         ("permuted_element_producer", PermutedElementProducer(), (rn(7, 24, 5, 16),)),
         ("permuted_row_value", PermutedRowValue(), (rn(16, 3, 64, 5), rn(3, 64, 1))),
+        ("layer_norm_row_matches_trailing", LayerNormRowMatchesTrailing(), (rn(1, 128, 128),)),
+        ("layer_norm_b2", LayerNormRowMatchesTrailing(), (rn(2, 128, 128),)),
     ]
 
 

@@ -20,7 +20,6 @@ import torch
 import fuzz_programs as fp
 from golden.dump_edge_cases import cases
 from mlc.api import build_pipeline
-from mlc.codegen.reduction_lowering import ReductionLoweringError
 from mlc.config import Config
 from mlc.ir.capture import capture
 from oracle import compile_reference
@@ -55,14 +54,30 @@ def _case(name):
     return next((m, a) for n, m, a in cases() if n == name)
 
 
-def test_edge_case_reference_errors_are_kept():
-    """A keepdim=False result whose shape right-aligns onto the element shape
-    is refused with the reference's error and message."""
-    model, args = _case("right_aligned_row_result")
-    kind, msg = FIXTURE["right_aligned_row_result"]["error"]
-    with pytest.raises(ReductionLoweringError) as e:
-        build_pipeline(capture(model, args), CFG)
-    assert kind == "ReductionLoweringError" and str(e.value) == msg
+@pytest.mark.parametrize("name", ["right_aligned_row_result", "layer_norm_row_matches_trailing"])
+def test_edge_cases_right_aligned_reduction_results(name):
+    """A keepdim=False reduction result whose shape also right-aligns onto the
+    element shape (``amax`` of ``[3, 3, 9, 128]`` over dim 1; the variance
+    inside LayerNorm over ``[1, 128, 128]``): the reference refuses the graph
+    (recorded ``ReductionLoweringError``); here the result is a row value, the
+    graph compiles to one kernel per reduction and matches eager. The same
+    LayerNorm at batch 2 compiles in both, to the same schedule."""
+    from mlc.kernels import ReductionKernel
+
+    model, args = _case(name)
+    assert FIXTURE[name]["error"][0] == "ReductionLoweringError"
+    sched = build_pipeline(capture(model, args), CFG)
+    assert sum(isinstance(k, ReductionKernel) for k in sched.kernels) == 1
+    got = compile_reference(model, args, CFG)(*args)
+    with torch.no_grad():
+        want = model(*args)
+    assert fp.max_rel_error(got, want) <= (1e-5 if want.dtype == torch.float32 else 2e-2)
+    model, args = _case("layer_norm_b2")
+    rec = FIXTURE["layer_norm_b2"]
+    sched = build_pipeline(capture(model, args), CFG)
+    assert [k.summary() for k in sched.kernels] == [k["summary"] for k in rec["kernels"]]
+    assert [[[a.value.buffer.name, a.index.render()] for a in k.inputs] for k in sched.kernels] \
+        == [k["inputs"] for k in rec["kernels"]]
 
 
 def test_edge_case_row_output_reading_an_operand():
@@ -138,7 +153,8 @@ def test_random_programs_hip_matches_oracle(seed, cname):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["row_output_reads_operand", "reshaped_row_operand",
-                                  "permuted_element_producer", "permuted_row_value"])
+                                  "permuted_element_producer", "permuted_row_value",
+                                  "right_aligned_row_result", "layer_norm_row_matches_trailing"])
 def test_edge_cases_hip_matches_oracle(name):
     import mlc
 
@@ -190,3 +206,44 @@ def test_random_attention_hip_matches_oracle(seed):
     e_oracle, e_exact = fp.max_rel_error(got.cpu(), want), _fp64_err(got, model, args)
     print(f"  hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}", flush=True)
     assert e_oracle <= 2e-3 and e_exact <= 2e-3, desc
+
+
+EVERY = Config(cuda_graphs=False, merge_parallel_gemms=True, gemm_epilogue=True,
+               layout_selection=True, fused_attention=True)
+
+
+def _stack_bar(dtype) -> float:
+    return 1e-5 if dtype == torch.float32 else 2e-3
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_stacks_every_variant_oracle(seed):
+    """Random transformer stacks (``fuzz_programs.block_case``) under every
+    schedule variant against the reference schedule, both through the
+    oracle: within the fp32 bar, or 2e-3 of the largest output for fp16."""
+    model, args, desc = fp.block_case(seed)
+    base = compile_reference(model, args, CFG)(*args)
+    got = compile_reference(model, args, EVERY)(*args)
+    assert fp.max_rel_error(got, base) <= _stack_bar(got.dtype), desc
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(16))
+def test_random_stacks_hip_matches_oracle(seed):
+    """The same stacks on the GPU, reference schedule and every variant, each
+    against the oracle running the same schedule: within the fp32 bar, or
+    2e-3 of the largest output for fp16."""
+    import mlc
+
+    model, args, desc = fp.block_case(seed)
+    print(desc, flush=True)
+    wants = [compile_reference(model, args, cfg)(*args) for cfg in (CFG, EVERY)]
+    model = model.cuda()
+    dev = tuple(a.cuda() for a in args)
+    for cfg, want in zip((CFG, EVERY), wants):
+        got = mlc.compile(model, dev, cfg)(*dev)
+        torch.cuda.synchronize()
+        err = fp.max_rel_error(got.cpu(), want)
+        print(f"  {'every variant' if cfg is EVERY else 'reference'}: hip-vs-oracle {err:.2e}",
+              flush=True)
+        assert err <= _stack_bar(got.dtype), desc
