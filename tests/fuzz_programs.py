@@ -422,3 +422,44 @@ def block_case(seed: int):
     desc = (f"{style} b{b} T{t} d{d} h{h} {act} bias={bias} layers={layers} "
             f"{str(dtype).replace('torch.', '')}")
     return model, (x, keep), desc
+
+
+def extern_case(seed: int):
+    """Random chains through the extern ops (``mm``, ``bmm``, ``addmm``,
+    ``matmul``, ``linear``) on transposed, sliced and expanded operands, with
+    pointwise and reduction kernels around them: (model, inputs,
+    description). Sizes 8..96; fp32 or fp16."""
+    rng = random.Random(3000 + seed)
+    dtype = rng.choice([torch.float32, torch.float16])
+    m, k, n = (rng.choice([8, 16, 24, 33, 64, 96]) for _ in range(3))
+    bt = rng.choice([1, 2, 3])
+    kind = rng.choice(["mm_t", "mm_slice", "bmm_t", "addmm", "matmul_bcast", "linear"])
+    g = torch.Generator().manual_seed(seed)
+
+    def rn(*s):
+        return (torch.randn(*s, generator=g) * 0.3).to(dtype)
+
+    if kind == "mm_t":          # B given as [n, k], read transposed
+        args = (rn(m, k), rn(n, k))
+        fn = lambda a, b: torch.tanh(a * 1.5) @ b.t()
+    elif kind == "mm_slice":    # every other column of A, a row slice of B
+        args = (rn(m, 2 * k), rn(k + 3, n))
+        fn = lambda a, b: torch.relu(a[:, ::2] @ b[1:k + 1]) + 0.5
+    elif kind == "bmm_t":
+        args = (rn(bt, m, k), rn(bt, n, k))
+        fn = lambda a, b: (a @ b.transpose(1, 2)).softmax(dim=-1)
+    elif kind == "addmm":
+        args = (rn(m, k), rn(k, n), rn(n))
+        fn = lambda a, b, c: torch.addmm(c, a, b) * 2.0
+    elif kind == "matmul_bcast":  # a batch of A against one B
+        args = (rn(bt, m, k), rn(k, n))
+        fn = lambda a, b: F.layer_norm(torch.matmul(a, b), (n,)) if n > 1 else torch.matmul(a, b)
+    else:
+        args = (rn(bt, m, k), rn(n, k), rn(n))
+        fn = lambda a, w, c: F.gelu(F.linear(a, w, c)).sum(dim=-1)
+
+    class Ext(torch.nn.Module):
+        def forward(self, *xs):
+            return fn(*xs)
+
+    return Ext(), args, f"{kind} m{m} k{k} n{n} b{bt} {str(dtype).replace('torch.', '')}"

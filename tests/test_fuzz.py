@@ -247,3 +247,76 @@ def test_random_stacks_hip_matches_oracle(seed):
         print(f"  {'every variant' if cfg is EVERY else 'reference'}: hip-vs-oracle {err:.2e}",
               flush=True)
         assert err <= _stack_bar(got.dtype), desc
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_extern_chains_oracle_matches_eager(seed):
+    """Library GEMMs on transposed, sliced and broadcast operands with
+    generated kernels around them, through the oracle, against eager."""
+    model, args, desc = fp.extern_case(seed)
+    got = compile_reference(model, args, CFG)(*args)
+    with torch.no_grad():
+        want = model(*args)
+    assert fp.max_rel_error(got, want) <= (1e-5 if want.dtype == torch.float32 else 2e-2), desc
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(24))
+def test_extern_chains_hip_matches_oracle(seed):
+    """The extern chains on the GPU (hipBLASLt through PyTorch, bound ``out=``
+    into the arena, or called and copied) against the oracle: within the fp32
+    bar, or 2e-3 of the largest output for fp16."""
+    import mlc
+
+    model, args, desc = fp.extern_case(seed)
+    want = compile_reference(model, args, CFG)(*args)
+    dev = tuple(a.cuda() for a in args)
+    got = mlc.compile(model, dev, CFG)(*dev)
+    torch.cuda.synchronize()
+    err = fp.max_rel_error(got.cpu(), want)
+    print(f"{desc}: hip-vs-oracle {err:.2e}", flush=True)
+    assert err <= (1e-5 if want.dtype == torch.float32 else 2e-3), desc
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", [("program", 0), ("program", 1), ("program", 2),
+                                  ("wide", 0), ("extern", 3), ("extern", 23),
+                                  ("stack", 0), ("stack", 8)])
+def test_random_graph_replays(case):
+    """The product path: ``Config()`` captures the forward in one hipGraph and
+    replays it. Three calls with new inputs each, eager work on the device in
+    between; every replay against the oracle on the same inputs, and a
+    repeated input reproduces its first result bit for bit."""
+    import mlc
+
+    kind, seed = case
+    if kind in ("program", "wide"):
+        model, args = fp.program(seed, wide=kind == "wide")
+        bar = lambda c: fp.tolerance(c)  # noqa: E731
+        chains = model.chains
+    elif kind == "extern":
+        model, args, _ = fp.extern_case(seed)
+        chains = None
+    else:
+        model, args, _ = fp.block_case(seed)
+        chains = None
+    cfg = Config()
+    oracle = compile_reference(model, args, Config(cuda_graphs=False))
+    calls = [args, tuple(a * 0.5 if a.is_floating_point() else a for a in args), args]
+    wants = [tuple(t.clone() for t in _tuple(oracle(*c))) for c in calls]
+    if kind == "stack":
+        model = model.cuda()
+    compiled = mlc.compile(model, tuple(a.cuda() for a in args), cfg)
+    outs = []
+    for c, want in zip(calls, wants):
+        got = tuple(t.clone() for t in _tuple(compiled(*(a.cuda() for a in c))))
+        junk = torch.randn(1 << 20, device="cuda").sin_().sum()  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
+        outs.append(got)
+        for i, (g, w) in enumerate(zip(got, want)):
+            limit = bar(chains[i]) if chains else (1e-5 if w.dtype == torch.float32 else 2e-3)
+            assert fp.max_rel_error(g.cpu(), w) <= limit, (kind, seed, i)
+    assert compiled._captured, "the forward was not captured into a hipGraph"
+    for g0, g2 in zip(outs[0], outs[2]):
+        assert torch.equal(g0, g2)
