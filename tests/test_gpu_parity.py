@@ -83,12 +83,17 @@ class _Unary(torch.nn.Module):
         return self.fn(x)
 
 
-@pytest.mark.parametrize("fn,lo,hi", [(torch.exp, -87.0, 88.0), (torch.erf, -6.0, 6.0),
-                                      (torch.exp, -1.0, 1.0), (torch.erf, -1.0, 1.0)])
-def test_device_exp_erf_error_bound(fn, lo, hi):
-    """exp and erf as the kernels evaluate them (ROCm device math) against
-    float64: at most 2 ulp over a dense grid, and torch's behaviour on the
-    special values (inf, nan, signed zero)."""
+@pytest.mark.parametrize("fn,lo,hi,bound", [
+    (torch.exp, -87.0, 88.0, 2.0), (torch.erf, -6.0, 6.0, 2.0), (torch.exp, -1.0, 1.0, 2.0),
+    (torch.erf, -1.0, 1.0, 2.0), (torch.tanh, -10.0, 10.0, 2.0), (torch.sin, -100.0, 100.0, 2.0),
+    (torch.cos, -100.0, 100.0, 2.0), (torch.log, 1e-6, 1e6, 2.0), (torch.sqrt, 0.0, 1e6, 0.5),
+    (torch.rsqrt, 1e-6, 1e6, 1.5), (torch.sigmoid, -80.0, 30.0, 3.0)])
+def test_device_transcendental_error_bound(fn, lo, hi, bound):
+    """Every transcendental the kernels evaluate (ROCm device math: exp, erf,
+    tanh, sin, cos, log; sqrt correctly rounded; rsqrt as 1/sqrt, two
+    roundings; sigmoid as 1/(1+exp(-x))) against float64: within ``bound``
+    ulp over a dense grid, and torch's behaviour on the special values (inf,
+    nan, signed zero, negative arguments)."""
     inf, nan = float("inf"), float("nan")
     special = torch.tensor([0.0, -0.0, inf, -inf, nan, 1e-30, -1e-30, 0.875, -0.875,
                             0.87499994, 4.0, 3.9, -3.9, 88.7, 89.5, -103.9, -200.0, 1e-7])
@@ -111,7 +116,7 @@ def test_device_exp_erf_error_bound(fn, lo, hi):
     err = ((got.double() - want).abs() / ulp)[normal]
     print(f"{fn.__name__} [{lo}, {hi}]: max {err.max().item():.3f} ulp, "
           f"mean {err.mean().item():.3f}")
-    assert err.max().item() <= 2.0
+    assert err.max().item() <= bound
 
 
 class _Ragged(torch.nn.Module):
