@@ -4,7 +4,8 @@
         python mlc-compiler_amd/mlc/bench/traffic.py
     rocprofv3 --pmc WRITE_SIZE ... (same)
 
-It launches, ``--iters`` times each:
+It launches, ``--iters`` times each (with ``--kernel all``, each kernel after
+the plan is replayed up to it, so on its real inputs):
 
 1. a plain device copy of ``--copy-mib`` MiB (torch ``copy_``), whose true
    traffic is known (that many bytes read and written): the counters' scale
@@ -17,7 +18,8 @@ It launches, ``--iters`` times each:
    on (``merge_parallel_gemms``, ``gemm_epilogue``, ``layout_selection``,
    ``fused_attention``); with ``--kernel all``, every generated kernel of
    the reference schedule at config 4 (for per-kernel counters such as
-   ``SQ_INSTS_VALU``). ``--workload`` picks another configuration (default
+   ``SQ_INSTS_VALU``), or of the schedule with every variant on with
+   ``--config every``. ``--workload`` picks another configuration (default
    config 4).
 
 It prints each kernel's symbol and algorithmic bytes per launch so the
@@ -42,6 +44,8 @@ def main() -> int:
     ap.add_argument("--copy-mib", type=int, default=1024)
     ap.add_argument("--kernel", choices=("gelu", "attention", "all"), default="gelu")
     ap.add_argument("--workload", default="C4", help="workload key (default C4)")
+    ap.add_argument("--config", choices=("reference", "every"), default="reference",
+                    help="schedule for --kernel all: the reference's, or every variant on")
     opts = ap.parse_args()
 
     import torch
@@ -51,6 +55,7 @@ def main() -> int:
     from mlc.bench.workloads import make
     from mlc.config import Config
     from mlc.kernels import AttentionKernel, PointwiseKernel
+    from mlc.runtime.executor import run_bound_extern
 
     torch.cuda.set_device(0)
     n = opts.copy_mib * (1 << 20) // 2
@@ -77,6 +82,9 @@ def main() -> int:
             return isinstance(k, AttentionKernel)
     else:
         cfg = Config(cuda_graphs=False)
+        if opts.config == "every":
+            cfg = Config(cuda_graphs=False, merge_parallel_gemms=True, gemm_epilogue=True,
+                         layout_selection=True, fused_attention=True)
 
         def wanted(k):
             return True
@@ -84,11 +92,22 @@ def main() -> int:
     compiled(*inputs)
     torch.cuda.synchronize()
     rt = compiled._module
-    found = [(k, p) for k, (kind, p) in zip(compiled.schedule.kernels, compiled._plan)
+    plan = compiled._plan
+    found = [(i, k, p) for i, (k, (kind, p)) in enumerate(zip(compiled.schedule.kernels, plan))
              if kind == "kernel" and wanted(k)]
     if opts.kernel != "all":
         found = found[-1:]
-    for k, bound in found:
+    replayed = 0
+    for i, k, bound in found:
+        if opts.kernel == "all":
+            # the plan up to this kernel first, so it runs on its real inputs
+            # (the arena's slots are reused; erf's work depends on its data)
+            for kind_j, payload_j in plan[replayed:i]:
+                if kind_j == "extern":
+                    run_bound_extern(payload_j)
+                else:
+                    rt.run_bound(payload_j)
+            replayed = i
         for _ in range(opts.iters):
             rt.run_bound(bound)
         torch.cuda.synchronize()

@@ -155,6 +155,24 @@ def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc:
     return load, store
 
 
+#: XCDs of one MI355X; workgroups are dispatched to them round-robin by index
+XCDS = 8
+
+
+def _tile_of_workgroup(BH: int, NQB: int, QB: int, it: str) -> list[str]:
+    """``bh`` and ``q0`` of this workgroup. Workgroup ``i`` runs on XCD
+    ``i % 8``, and every XCD has its own L2. When a head has several query
+    tiles and the heads divide evenly over the XCDs, a head's tiles are given
+    to workgroups on one XCD, so its keys and values are fetched into one L2
+    once rather than into several."""
+    if NQB > 1 and BH % XCDS == 0:
+        return [f"  const uint32_t xcd = blockIdx.x % {XCDS}, slot = blockIdx.x / {XCDS};",
+                f"  const {it} bh = ({it})((slot / {NQB}) * {XCDS} + xcd);",
+                f"  const int q0 = (int)(slot % {NQB}) * {QB};"]
+    return [f"  const {it} bh = ({it})(blockIdx.x / {NQB});",
+            f"  const int q0 = (int)(blockIdx.x % {NQB}) * {QB};"]
+
+
 def _aligned(offset: int, strides) -> bool:
     return offset % 8 == 0 and all(s % 8 == 0 for s in strides)
 
@@ -188,8 +206,7 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     L.append(f"  __shared__ __align__(16) mlc::f16 ks[{Tk * PK}];")
     L.append(f"  __shared__ __align__(16) mlc::f16 vt[{D * PV}];")
     L.append(f"  __shared__ __align__(16) mlc::f16 qs[{QB * PQ}];")
-    L.append(f"  const {it} bh = ({it})(blockIdx.x / {NQB});")
-    L.append(f"  const int q0 = (int)(blockIdx.x % {NQB}) * {QB};")
+    L += _tile_of_workgroup(BH, NQB, QB, it)
 
     ql_ = k.q.layout
     qsb, qsr, qsc = ql_.strides
@@ -454,8 +471,7 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append(f"  __shared__ __align__(16) mlc::f16 ks[{KB * PK}];")
     L.append(f"  __shared__ __align__(16) mlc::f16 vt[{D * PV}];")
     L.append(f"  __shared__ __align__(16) mlc::f16 qs[{QB * PQ}];")
-    L.append(f"  const {it} bh = ({it})(blockIdx.x / {NQB});")
-    L.append(f"  const int q0 = (int)(blockIdx.x % {NQB}) * {QB};")
+    L += _tile_of_workgroup(BH, NQB, QB, it)
     ql_ = k.q.layout
     qsb, qsr, qsc = ql_.strides
     rows_valid = None
