@@ -820,7 +820,8 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             raise AssertionError("vector temp read in a row-scalar expression")
         return name, temp_types[name]
 
-    elem_r = Renderer(ref_elem, temp_elem)
+    nonpos = nonpositive_args(k)
+    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos)
     scal_r = Renderer(ref_scalar, temp_scalar)
     rcp_for = _reciprocal_divisors(k, vector)
 
@@ -837,8 +838,9 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
                 sd = _scalar_division(s.expr, rcp_for)
                 if sd is not None and t == "float":
                     num, d = elem_r(sd[0])[0], sd[1]
+                    div = "div_rcp_finite" if _bounded_exp(sd[0], k, nonpos) else "div_rcp"
                     L.append(f"  if (__all(ok_{d})) {{")
-                    L += elem_loop(s.name, f"mlc::div_rcp({num}, {d}, rcp_{d})")
+                    L += elem_loop(s.name, f"mlc::{div}({num}, {d}, rcp_{d})")
                     L.append("  } else {")
                     L += elem_loop(s.name, code)
                     L.append("  }")
@@ -930,6 +932,60 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
                                           "lanes_per_row": G, "packs": K, "rows_per_wg": RPW,
                                           "rows": R, "cols": C})
     return "\n".join(L), spec
+
+
+def nonpositive_args(k: ReductionKernel) -> set[Expr]:
+    """Expressions that are ``x - rowmax(x)`` in ``k`` (a ``sub`` whose second
+    operand is a max reduce of its first, and the binds holding one): never
+    positive, so their ``exp`` needs no overflow path (``mlc::exp_nonpos``)."""
+    maxes = {s.name: s.expr for s in k.steps if isinstance(s, Reduce) and s.kind == "max"}
+    out: set[Expr] = set()
+
+    def is_sub(e) -> bool:
+        return (isinstance(e, Call) and e.fn == "sub" and isinstance(e.args[1], Ref)
+                and maxes.get(e.args[1].name) == e.args[0])
+
+    for s in k.steps:
+        if isinstance(s, Bind) and is_sub(s.expr):
+            out.add(s.expr)
+            out.add(Ref(s.name))
+    for s in k.steps:
+        for e in _subexprs(s.expr):
+            if is_sub(e):
+                out.add(e)
+    return out
+
+
+def _subexprs(e):
+    yield e
+    if isinstance(e, Call):
+        for a in e.args:
+            yield from _subexprs(a)
+    elif isinstance(e, Cast):
+        yield from _subexprs(e.x)
+
+
+def _bounded_exp(e: Expr, k: ReductionKernel, nonpos: set) -> bool:
+    """``e`` is ``exp`` of a never-positive argument (or a bind holding one):
+    at most 1, never infinite."""
+    if isinstance(e, Ref):
+        e = next((s.expr for s in k.steps if isinstance(s, Bind) and s.name == e.name), None)
+    return isinstance(e, Call) and e.fn == "exp" and e.args[0] in nonpos
+
+
+class _NonPosExpRenderer(Renderer):
+    """``exp`` of an argument known to be at most 0 as ``mlc::exp_nonpos``."""
+
+    def __init__(self, operand, temp, nonpos: set) -> None:
+        super().__init__(operand, temp)
+        self.nonpos = nonpos
+
+    def call(self, e: Call) -> tuple[str, str]:
+        if e.fn == "exp" and e.args[0] in self.nonpos:
+            code, t = self(e.args[0])
+            if t == "float":
+                return f"mlc::exp_nonpos({code})", "float"
+        return super().call(e)
 
 
 def _reciprocal_divisors(k: ReductionKernel, vector: set[str]) -> set[str]:

@@ -140,6 +140,18 @@ __device__ __forceinline__ float exp_(float x) { return expf(x); }
 __device__ __forceinline__ float exp_fast(float x) {
   return __builtin_amdgcn_exp2f(x * 0x1.715476p+0f);
 }
+// exp(x) for x <= 0, -inf or NaN: a softmax's exp(x - rowmax(x)). With
+// x log2 e = n + f (n = rint, so |f| <= 1/2), f is formed with one rounding
+// from the exact product (fma) plus the low word of log2 e, 2^f comes from
+// v_exp_f32 and 2^n from ldexp (Cody and Waite's reduction). There is no
+// overflow to guard: x is at most 0, clamped below at -104 where exp is 0 in
+// fp32 (the NaN-propagating maximum keeps NaN, whose exponent is taken as 0).
+__device__ __forceinline__ float exp_nonpos(float x) {
+  x = __builtin_elementwise_maximum(x, -104.0f);
+  const float n = __builtin_rintf(x * 0x1.715476p+0f);
+  const float f = __builtin_fmaf(x, 0x1.4ae0c0p-26f, __builtin_fmaf(x, 0x1.715476p+0f, -n));
+  return __builtin_ldexpf(__builtin_amdgcn_exp2f(f), (int)__builtin_fminf(n, 0.0f));
+}
 __device__ __forceinline__ double exp_(double x) { return exp(x); }
 __device__ __forceinline__ float erf_(float x) { return erff(x); }
 __device__ __forceinline__ float log_(float x) { return logf(x); }
@@ -204,6 +216,12 @@ __device__ __forceinline__ float div_rcp(float x, float d, float y) {
   const float r = __builtin_fmaf(-q, d, x);
   const float q2 = __builtin_fmaf(r, y, q);
   return q2 == q2 ? q2 : q;
+}
+// div_rcp for an x that is never infinite (a softmax's exp(x - rowmax), at
+// most 1): the same quotient without the guard for an infinite x.
+__device__ __forceinline__ float div_rcp_finite(float x, float d, float y) {
+  const float q = x * y;
+  return __builtin_fmaf(__builtin_fmaf(-q, d, x), y, q);
 }
 // whether div_rcp is exact for every x with this divisor
 __device__ __forceinline__ bool rcp_ok(float d) {

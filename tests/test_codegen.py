@@ -191,3 +191,26 @@ def test_copy_ceiling_kernel_cross_compiles(tmp_path, monkeypatch):
     monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
     _, obj = native.compile_code_object(SOURCE)
     assert obj.stat().st_size > 0
+
+
+def test_softmax_exp_has_no_overflow_path():
+    """``exp(x - rowmax(x))`` never sees a positive argument: the reduction
+    kernel calls ``mlc::exp_nonpos`` for it and divides by the row sum without
+    the infinite-numerator guard; an ``exp`` of anything else keeps ``expf``."""
+    import torch.nn as nn
+
+    from mlc.api import build_pipeline
+    from mlc.codegen.hip_backend import generate_module
+    from mlc.config import Config
+    from mlc.ir.capture import capture
+
+    class Soft(nn.Module):
+        def forward(self, x):
+            return x.softmax(dim=-1), torch.exp(x).sum(dim=-1)
+
+    x = torch.randn(8, 64)
+    cfg = Config(cuda_graphs=False)
+    src = generate_module(build_pipeline(capture(Soft(), (x,)), cfg), cfg).source
+    body = src[src.index('extern "C"'):]
+    assert "mlc::exp_nonpos(" in body and "mlc::div_rcp_finite(" in body
+    assert "mlc::exp_(" in body

@@ -119,6 +119,41 @@ def test_device_transcendental_error_bound(fn, lo, hi, bound):
     assert err.max().item() <= bound
 
 
+class _ShiftedExp(torch.nn.Module):
+    def forward(self, x):
+        return torch.exp(x - x.amax(dim=-1, keepdim=True))
+
+
+def test_softmax_exp_error_bound():
+    """A softmax's ``exp(x - rowmax(x))`` (``mlc::exp_nonpos``: argument never
+    positive, no overflow path) against float64: within 2 ulp over a dense
+    grid of [-104, 0], 0 for -inf, NaN for a row holding NaN. Every row's
+    maximum is 0, so the kernel's argument is the grid value itself."""
+    rows = 1024
+    grid = torch.linspace(-104.0, 0.0, rows * 1023)
+    x = torch.cat([torch.zeros(rows, 1), grid.view(rows, 1023)], dim=1)
+    x[5, 7] = float("-inf")
+    x[9, 3] = float("nan")
+    compiled = mlc.compile(_ShiftedExp(), (x.cuda(),), Config(cuda_graphs=False))
+    src = compiled._module.source_text
+    assert "mlc::exp_nonpos(" in src and "mlc::exp_(" not in src
+    got = compiled(x.cuda()).cpu()
+    torch.cuda.synchronize()
+    assert got[5, 7] == 0.0 and torch.isnan(got[9]).all()
+    ok = torch.ones_like(x, dtype=torch.bool)
+    ok[5, 7] = False
+    ok[9] = False
+    want = torch.exp(x.double())
+    w32 = want.float()
+    normal = ok & (w32 >= 2.0 ** -126)
+    ulp = (torch.nextafter(w32, torch.tensor(float("inf"))) - w32).double()
+    err = ((got.double() - want).abs() / ulp)[normal]
+    print(f"exp_nonpos [-104, 0]: max {err.max().item():.3f} ulp, mean {err.mean().item():.3f}")
+    assert err.max().item() <= 2.0
+    sub = ok & (w32 < 2.0 ** -126)
+    assert ((got - w32).abs()[sub] <= 2.0 ** -148).all()
+
+
 class _Ragged(torch.nn.Module):
     """Softmax, LayerNorm, variance and a GELU chain over awkward sizes."""
 
