@@ -19,17 +19,25 @@ This restates the reference's torch backend
   (``:182-233``).
 
 Pinning (what fixes this oracle independently of itself):
-* end-to-end equality with eager PyTorch on every toy model and on the small
-  bench models at the reference's tolerances (rtol 1e-5 / atol 1e-6 fp32),
-  ``tests/test_oracle.py`` and ``tests/test_correctness.py``;
+* end-to-end equality with eager PyTorch on every toy model under every pass
+  configuration at the reference's tolerances (rtol 1e-5 / atol 1e-6 fp32),
+  and the reference's own torch-backend outputs for the same inputs
+  (fixtures it wrote), ``tests/test_oracle.py``;
+* seeded random programs (pointwise chains, views, casts, reductions, extern
+  GEMMs, transformer stacks) against eager PyTorch, ``tests/test_fuzz.py``;
 * the reference's index-rendering known answers (``tests/test_codegen.py``);
 * numerical special cases from the reference's tests: two-pass variance
-  against float64, large-mean layer norm, softmax on logits x100, masked max
-  identity (``tests/test_reduction_fusion.py``);
+  against float64, large-mean layer norm, softmax on logits x100, and planted
+  mistakes (a sign, exp2 for exp, a reduce identity) that must be caught
+  (``tests/test_oracle.py``);
 * streamed evaluation agrees with persistent evaluation.
-Transcendentals (exp/erf/tanh) are torch's CPU implementations: per-function
-parity against the reference's device libm is "parity unpinned"; only the
-end-to-end tolerances pin them, as in the reference.
+One deliberate difference from the reference's torch backend: a reduction's
+row output is evaluated at one column, as the reference's Triton kernels
+compute it (``run_reduction``); the torch backend fails on a row output that
+reads a row-constant operand.
+Transcendentals (exp/erf/tanh/...) are torch's CPU implementations:
+per-function parity against the reference's device libm is "parity
+unpinned"; only the end-to-end tolerances pin them, as in the reference.
 """
 
 from __future__ import annotations
