@@ -87,7 +87,8 @@ def test_oracle_matches_reference_backend_outputs(golden, name, cname):
 @pytest.mark.parametrize("name", [m[0] for m in all_models()])
 def test_exactness_classes_are_bit_identical(name):
     """Configs without reduction fusion evaluate the same ops in the same
-    order: results agree bit for bit (``tests/test_correctness.py:51-74``)."""
+    order: results agree bit for bit (the reference's
+    ``tests/test_correctness.py:51-74``)."""
     _, model, args = _model(name)
     base = compile_reference(model, args, CONFIGS["no_fusion"])(*args)
     for c in ("elementwise", "elementwise_recompute", "planned"):
