@@ -125,10 +125,16 @@ def test_edge_case_permuted_producer_is_not_fused():
 
 GPU_CASES = [(s, "default") for s in range(16)] + [(s, "streamed") for s in range(6)] + \
     [(s, "layout") for s in range(4)] + [(s, "wide") for s in range(6)] + \
-    [(s, "wide_streamed") for s in range(3)]
+    [(s, "wide_streamed") for s in range(3)] + [(s, "no_fusion") for s in range(2)] + \
+    [(s, "elementwise") for s in range(2)] + [(s, "unplanned") for s in range(2)]
 GPU_CONFIGS = {"default": CFG, "streamed": Config(cuda_graphs=False, max_persistent_row=16),
                "layout": Config(cuda_graphs=False, layout_selection=True), "wide": CFG,
-               "wide_streamed": Config(cuda_graphs=False, max_persistent_row=512)}
+               "wide_streamed": Config(cuda_graphs=False, max_persistent_row=512),
+               "no_fusion": Config(elementwise_fusion=False, recompute=False,
+                                   reduction_fusion=False, memory_planning=False,
+                                   cuda_graphs=False),
+               "elementwise": Config(reduction_fusion=False, cuda_graphs=False),
+               "unplanned": Config(memory_planning=False, cuda_graphs=False)}
 
 
 @pytest.mark.gpu
@@ -320,3 +326,17 @@ def test_random_graph_replays(case):
     assert compiled._captured, "the forward was not captured into a hipGraph"
     for g0, g2 in zip(outs[0], outs[2]):
         assert torch.equal(g0, g2)
+
+
+@pytest.mark.parametrize("cname", ["no_fusion", "elementwise", "unplanned"])
+def test_random_programs_under_every_pass_configuration(cname):
+    """The pass toggles (no fusion at all, elementwise fusion only, no arena
+    planning) compute the same function: through the oracle against the
+    default configuration's oracle, within five times the chain's bar (an
+    unfused schedule stores, and so rounds, narrow intermediates that a fused
+    kernel keeps in fp32)."""
+    model, args = fp.program(11)
+    base = _tuple(compile_reference(model, args, CFG)(*args))
+    got = _tuple(compile_reference(model, args, GPU_CONFIGS[cname])(*args))
+    for c, g, w in zip(model.chains, got, base):
+        assert fp.max_rel_error(g, w) <= fp.tolerance(c) * 5, (cname, c.shape, c.dtype)
