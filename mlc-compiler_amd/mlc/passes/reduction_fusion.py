@@ -8,10 +8,13 @@ column axis.
 
 Reference behaviour followed: ``mlc/passes/reduction_fusion.py:55-379``:
 frame classification, storability, the legality checks and the fixed-point
-growth loop with its neighbour visiting order. One check is added: a merge is
-refused when a member would read another member's value through an index map
-other than the one the kernel holds it at (the reference groups such
-producers and its kernel reads memory it never wrote).
+growth loop with its neighbour visiting order. Two changes, each only where
+the reference fails: a merge is refused when a member would read another
+member's value through an index map other than the one the kernel holds it at
+(the reference groups such producers and its kernel reads memory it never
+wrote); and a reduction's own result is classified by its producer, not by
+its shape alone (``classify_value``; the reference refuses graphs where that
+shape also right-aligns onto the element shape).
 """
 
 from __future__ import annotations
