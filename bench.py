@@ -117,7 +117,7 @@ def _kernel_table(compiled, iters: int):
         for kind_j, payload_j in plan[replayed:i]:
             if kind_j == "extern":
                 run_bound_extern(payload_j)
-            else:
+            elif kind_j == "kernel":
                 rt.run_bound(payload_j)
         replayed = i
         bound = payload if kind == "kernel" else payload[2]

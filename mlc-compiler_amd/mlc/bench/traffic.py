@@ -105,7 +105,7 @@ def main() -> int:
             for kind_j, payload_j in plan[replayed:i]:
                 if kind_j == "extern":
                     run_bound_extern(payload_j)
-                else:
+                elif kind_j == "kernel":
                     rt.run_bound(payload_j)
             replayed = i
         for _ in range(opts.iters):

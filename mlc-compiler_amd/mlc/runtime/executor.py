@@ -65,6 +65,13 @@ class CompiledModel:
 
         self._arena: torch.Tensor | None = None
         self._live = self._live_buffers()
+        # externs reading no tensor (``aten.scalar_tensor``, ``full``, ...):
+        # their result never changes, so they run once when the plan is
+        # built, into memory of their own, and are not replayed. One that
+        # allocates (no ``out=`` form) would otherwise allocate inside the
+        # captured graph.
+        self._constants = {k.name for k in schedule.kernels
+                           if isinstance(k, ExternKernel) and not k.reads()}
         self._resident: dict[str, torch.Tensor] | None = None
         self._plan: list | None = None
         self._runs: list | None = None
@@ -142,6 +149,10 @@ class CompiledModel:
             for v in self.graph.inputs:
                 buffers[v.buffer.name] = torch.empty(v.buffer.numel, dtype=v.dtype,
                                                      device=self.device)
+            for k in self.schedule.kernels:
+                if k.name in self._constants:
+                    for v in k.writes():
+                        buffers.setdefault(v.buffer.name, self._empty(v.buffer))
             self._bind_arena(buffers)
             self._resident = buffers
             self._static_inputs_flat = [buffers[v.buffer.name] for v in self.graph.inputs]
@@ -153,7 +164,11 @@ class CompiledModel:
     def _build_plan(self, buffers: dict[str, torch.Tensor]) -> list:
         plan: list = []
         for k in self.schedule.kernels:
-            if isinstance(k, ExternKernel):
+            if k.name in self._constants:
+                bound = bind_extern(k, buffers, self._module)
+                run_bound_extern(bound)
+                plan.append(("const", bound))
+            elif isinstance(k, ExternKernel):
                 plan.append(("extern", bind_extern(k, buffers, self._module)))
             else:
                 plan.append(("kernel", self._module.bind(k, buffers)))
@@ -174,7 +189,7 @@ class CompiledModel:
         for kind, payload in self._runs:
             if kind == "extern":
                 run_bound_extern(payload)
-            else:
+            elif kind == "kernel":
                 run(payload)
 
     def run_one(self, k, buffers: dict[str, torch.Tensor]) -> None:
@@ -272,7 +287,7 @@ class CompiledModel:
                 before = _alloc_count(self.device)
                 if kind == "extern":
                     run_bound_extern(payload)
-                else:
+                elif kind == "kernel":
                     self._module.run_bound(payload)
                 if _alloc_count(self.device) != before:
                     found.append(kernel.summary())

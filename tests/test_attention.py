@@ -226,3 +226,65 @@ def test_long_rows_use_the_key_blocked_kernel():
     assert "m_run" in body and "l_run" in body and "mlc::exp_fast" in body
     assert body.count("__syncthreads();") == 3
     assert sched.arena_bytes < base.arena_bytes // 2
+
+
+class _NoMask(nn.Module):
+    def forward(self, q, k, v):
+        return ((q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1])).softmax(-1) @ v
+
+
+class _WhereMask(nn.Module):
+    def forward(self, q, k, v, keep):
+        s = (q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1])
+        s = torch.where(keep, s, torch.tensor(torch.finfo(torch.float16).min, dtype=s.dtype))
+        return s.softmax(-1) @ v
+
+
+class _Fp32Softmax(nn.Module):
+    def forward(self, q, k, v):
+        s = (q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1])
+        return s.float().softmax(-1).half() @ v
+
+
+class _ScaledQ(nn.Module):
+    def forward(self, q, k, v):
+        return ((q * (1.0 / math.sqrt(q.shape[-1]))) @ k.transpose(-2, -1)).softmax(-1) @ v
+
+
+class _MaskedFill(nn.Module):
+    def forward(self, q, k, v, keep):
+        s = (q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1])
+        return s.masked_fill(~keep, float("-inf")).softmax(-1) @ v
+
+
+def attention_patterns(t=128, tk=128):
+    """How models write attention: no mask, a boolean causal mask through
+    ``where`` or ``masked_fill``, the softmax in fp32, the scale on q."""
+    q, k, v, _ = _inputs(2, 4, t, tk, 64)
+    keep = torch.tril(torch.ones(t, tk, dtype=torch.bool), diagonal=tk - t)[None, None]
+    return [("no_mask", _NoMask(), (q, k, v)), ("where_bool", _WhereMask(), (q, k, v, keep)),
+            ("fp32_softmax", _Fp32Softmax(), (q, k, v)), ("scaled_q", _ScaledQ(), (q, k, v)),
+            ("masked_fill", _MaskedFill(), (q, k, v, keep))]
+
+
+def exact_attention(name, args):
+    """float64 attention for a pattern of ``attention_patterns``."""
+    q, k, v = (a.double() for a in args[:3])
+    s = (q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1])
+    if len(args) > 3:
+        s = s.masked_fill(~args[3], float("-inf"))
+    return s.softmax(-1) @ v
+
+
+@pytest.mark.parametrize("tk", [128, 256])
+def test_common_attention_patterns_fuse(tk):
+    """Each way of writing attention becomes one attention kernel (single pass
+    at 128 keys, key-blocked at 256), and the oracle's fused kernel is within
+    2e-3 of float64."""
+    for name, model, args in attention_patterns(tk, tk):
+        sched = build_pipeline(capture(model, args), ATTN)
+        assert len(_attention(sched)) == 1, name
+        got = compile_reference(model, args, ATTN)(*args)
+        exact = exact_attention(name, args)
+        err = ((got.double() - exact).abs().max() / exact.abs().max()).item()
+        assert err <= 2e-3, (name, err)

@@ -94,3 +94,31 @@ def test_bench_refuses_more_than_one_gpu():
                           text=True, cwd=str(__import__("pathlib").Path(__file__).parents[1]))
     assert proc.returncode == 2
     assert "one GPU" in proc.stderr
+
+
+def test_externs_without_tensor_inputs_run_once_into_their_own_memory():
+    """``masked_fill`` with a float scalar exports ``aten.scalar_tensor``,
+    which has no ``out=`` form and allocates. An extern that reads no tensor
+    always gives the same result, so it runs once when the plan is built, into
+    a buffer of its own (not an arena slice another buffer may reuse), and is
+    never replayed: a captured forward then allocates nothing."""
+    from mlc.kernels import ExternKernel
+
+    class Fill(torch.nn.Module):
+        def forward(self, x):
+            return (x.masked_fill(x > 0.5, float("-inf")).softmax(-1) * 2.0).sum(-1)
+
+    x = torch.randn(8, 64)
+    compiled = compile_reference(Fill(), (x,), FULL)
+    got = compiled(x).clone()
+    assert [k.node.op for k in compiled.schedule.kernels if isinstance(k, ExternKernel)] == \
+        ["aten.scalar_tensor.default"]
+    kinds = [kind for kind, _ in compiled._plan]
+    assert kinds.count("const") == 1 and "extern" not in kinds
+    name = next(k for k in compiled.schedule.kernels if isinstance(k, ExternKernel)) \
+        .outputs[0].buffer.name
+    arena = compiled._arena
+    t = compiled._resident[name]
+    assert arena is None or not (arena.data_ptr() <= t.data_ptr() < arena.data_ptr() + arena.numel())
+    torch.testing.assert_close(got, Fill()(x))
+    torch.testing.assert_close(compiled(x * 3.0), Fill()(x * 3.0))

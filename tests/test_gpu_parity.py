@@ -568,3 +568,22 @@ def test_fused_attention_causal_mask_key_blocked(t):
     print(f"causal {t}: hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}")
     assert torch.isfinite(got).all()
     assert e_oracle <= 2e-3 and e_exact <= 2e-3
+
+
+@pytest.mark.parametrize("tk", [128, 256])
+def test_common_attention_patterns_on_the_gpu(tk):
+    """The MFMA kernels on each way of writing attention (no mask, boolean
+    causal mask through where / masked_fill, fp32 softmax, scaled q): within
+    2e-3 of the oracle's fused kernel and of float64."""
+    from test_attention import attention_patterns, exact_attention
+
+    for name, model, args in attention_patterns(tk, tk):
+        want = compile_reference(model, args, ATTN)(*args)
+        dev = tuple(a.cuda() for a in args)
+        compiled = mlc.compile(model, dev, ATTN)
+        assert [s.meta["kind"] for s in compiled._module.launch_table.values()].count("attention") == 1
+        got = compiled(*dev)
+        torch.cuda.synchronize()
+        e_oracle, e_exact = rel_err(got, want), rel_err(got, exact_attention(name, args))
+        print(f"{name} {tk}: hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}")
+        assert e_oracle <= 2e-3 and e_exact <= 2e-3, name
