@@ -659,17 +659,20 @@ def _prev_pow2(n: int) -> int:
 
 #: persistent-reduction shape: packs each lane holds (the widest lane group
 #: with ``min_packs <= K <= max_packs`` wins) and the workgroup size cap
-REDUCTION_TUNING = {"min_packs": 2, "max_packs": 8, "block": 128}
+#: ``few_rows``: at most this many rows (a batch-1 forward), a launch is latency-bound and
+#: each lane's serial chain matters more than per-lane reuse: one pack per lane is allowed
+REDUCTION_TUNING = {"min_packs": 2, "max_packs": 8, "block": 128, "few_rows": 4096}
 
 
 def reduction_geometry(n_rows: int, n_cols: int, V: int) -> dict:
     """Lanes per row G, packs per lane K, rows per workgroup."""
     t = REDUCTION_TUNING
     nvec = -(-n_cols // V)
+    min_packs = 1 if n_rows <= t["few_rows"] else t["min_packs"]
     G = None
     if nvec <= WAVE * t["max_packs"]:
         for g in (64, 32, 16, 8, 4, 2, 1):
-            if g <= nvec and nvec % g == 0 and t["min_packs"] <= nvec // g <= t["max_packs"]:
+            if g <= nvec and nvec % g == 0 and min_packs <= nvec // g <= t["max_packs"]:
                 G = g
                 break
         if G is None:
