@@ -1085,7 +1085,8 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
     def temp_scalar(name):
         return name, temp_types[name]
 
-    elem_r = Renderer(ref_elem, temp_elem)
+    nonpos = nonpositive_args(k)
+    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos)
     scal_r = Renderer(lambda s: (f"v{s}", in_types[s]), temp_scalar)
     rcp_for = _reciprocal_divisors(k, vector)
 
@@ -1129,9 +1130,10 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             sd = _scalar_division(b.expr, rcp_for)
             if sd is not None and t == "float":
                 num, d = elem_r(sd[0])[0], sd[1]
+                div = "div_rcp_finite" if _bounded_exp(sd[0], k, nonpos) else "div_rcp"
                 out.append(f"    if (__all(ok_{d})) {{")
                 out.append("#pragma unroll")
-                out.append(f"      for (int j = 0; j < V; ++j) {b.name}[j] = mlc::div_rcp({num}, {d}, rcp_{d});")
+                out.append(f"      for (int j = 0; j < V; ++j) {b.name}[j] = mlc::{div}({num}, {d}, rcp_{d});")
                 out.append("    } else {")
                 out.append("#pragma unroll")
                 out.append(f"      for (int j = 0; j < V; ++j) {b.name}[j] = {code};")
@@ -1145,8 +1147,9 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             out.append("    for (int j = 0; j < V; ++j) {")
             out.append(f"      const float x = (float)({code});")
             out.append("      const float m_new = mlc::max_<float>(m_run, x);")
-            out.append("      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : mlc::exp_(m_run - m_new);")
-            out.append("      l_run = l_run * alpha + mlc::exp_(x - m_new);")
+            # m_new is the max of m_run and x: both exponents are at most 0
+            out.append("      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : mlc::exp_nonpos(m_run - m_new);")
+            out.append("      l_run = l_run * alpha + mlc::exp_nonpos(x - m_new);")
             out.append("      m_run = m_new;")
             out.append("    }")
         else:
@@ -1174,7 +1177,7 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             mx, sm = online.max_step.name, online.sum_step.name
             slot = f"lds_{mx}" if need_lds else "nullptr"
             out.append(f"  const float {mx} = mlc::row_reduce<G, mlc::OpMax>(m_run, (float*){slot});")
-            out.append(f"  const float w_{sm} = (m_run == (-__builtin_huge_valf())) ? 0.0f : mlc::exp_(m_run - {mx});")
+            out.append(f"  const float w_{sm} = (m_run == (-__builtin_huge_valf())) ? 0.0f : mlc::exp_nonpos(m_run - {mx});")
             slot = f"lds_{sm}" if need_lds else "nullptr"
             out.append(f"  const float {sm} = mlc::row_reduce<G, mlc::OpSum>(l_run * w_{sm}, (float*){slot});")
             out += _reciprocal_lines(mx, rcp_for) + _reciprocal_lines(sm, rcp_for)
