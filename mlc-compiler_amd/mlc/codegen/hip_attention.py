@@ -37,6 +37,8 @@ reduction kernel, and the softmax's exp and division take fast forms
 
 from __future__ import annotations
 
+import torch
+
 from ..kernels import AttentionKernel, Bind
 from .hip_backend import (_IDENTITY, _OP, STORAGE, WAVE, LaunchSpec, Renderer, _RowOffsets,
                           _expr_varies, _params, _reciprocal_divisors, _reciprocal_lines,
@@ -80,6 +82,19 @@ class _FastExpRenderer(Renderer):
         return super().call(e)
 
 
+#: 16-bit element, 8- and 4-element vector types of the operands, per dtype
+_TYPES = {torch.float16: ("mlc::f16", "mlc::half8", "mlc::half4"),
+          torch.bfloat16: ("__bf16", "mlc::bf16x8", "mlc::bf16x4")}
+
+
+def _type_aliases(k: AttentionKernel) -> str:
+    """The kernel body is written over ``e16``/``v8``/``v4``; these bind them
+    to the operands' 16-bit float type (conversions to ``e16`` round to
+    nearest even, as the unfused schedule's stores do)."""
+    e, v8, v4 = _TYPES[k.q.dtype]
+    return f"  using e16 = {e};\n  using v8 = {v8};\n  using v4 = {v4};"
+
+
 def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc: int, pr: int,
            pc: int, aligned_c: bool, aligned_r: bool, threads: int, rows_valid: str | None,
            it: str, perm_r: bool = False) -> tuple[list[str], list[str]]:
@@ -102,7 +117,7 @@ def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc:
     n = R * C // per
     trips = -(-n // threads)
     full = n % threads == 0
-    ty = "mlc::half8" if per == 8 else "mlc::f16"
+    ty = "v8" if per == 8 else "e16"
     load.append(f"  {ty} {tag}[{trips}];")
     load.append("#pragma unroll")
     load.append(f"  for (int u = 0; u < {trips}; ++u) {{")
@@ -126,17 +141,17 @@ def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc:
     load.append(f"    {rc}")
     store.append(f"    {rc}")
     if per == 8:
-        load.append(f"    {guard}{tag}[u] = *reinterpret_cast<const mlc::half8*>({addr});")
+        load.append(f"    {guard}{tag}[u] = *reinterpret_cast<const v8*>({addr});")
         if mode == "c" and pc == 1 and pr % 8 == 0:
-            store.append(f"    {guard}*reinterpret_cast<mlc::half8*>({lds} + r * {pr} + c) = {tag}[u];")
+            store.append(f"    {guard}*reinterpret_cast<v8*>({lds} + r * {pr} + c) = {tag}[u];")
         elif mode == "r" and pr == 1 and pc % 8 == 0 and perm_r:
             # 8 keys starting at a multiple of 8 land as two runs of 4
             store.append(f"    {guard}{{")
-            store.append(f"      *reinterpret_cast<mlc::half4*>({lds} + mlc::vperm(r) + c * {pc}) = {tag}[u].lo;")
-            store.append(f"      *reinterpret_cast<mlc::half4*>({lds} + mlc::vperm(r + 4) + c * {pc}) = {tag}[u].hi;")
+            store.append(f"      *reinterpret_cast<v4*>({lds} + mlc::vperm(r) + c * {pc}) = {tag}[u].lo;")
+            store.append(f"      *reinterpret_cast<v4*>({lds} + mlc::vperm(r + 4) + c * {pc}) = {tag}[u].hi;")
             store.append("    }")
         elif mode == "r" and pr == 1 and pc % 8 == 0:
-            store.append(f"    {guard}*reinterpret_cast<mlc::half8*>({lds} + r + c * {pc}) = {tag}[u];")
+            store.append(f"    {guard}*reinterpret_cast<v8*>({lds} + r + c * {pc}) = {tag}[u];")
         else:
             if mode == "c":  # one row, 8 columns
                 row, col = rr, "(c + j)"
@@ -148,7 +163,7 @@ def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc:
                          f"= {tag}[u][j];")
             store.append("    }")
     else:
-        load.append(f"    {guard}{tag}[u] = {src}[{base} + ({it})r * ({it}){sr} + ({it})c * ({it}){sc}];")
+        load.append(f"    {guard}{tag}[u] = *reinterpret_cast<const e16*>({src} + {base} + ({it})r * ({it}){sr} + ({it})c * ({it}){sc});")
         store.append(f"    {guard}{lds}[{rr} * {pr} + c * {pc}] = {tag}[u];")
     load.append("  }")
     store.append("  }")
@@ -203,9 +218,10 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
              f"16 per wave")
     if FAST_SOFTMAX_MATH:
         L.append("#pragma clang fp contract(fast)")
-    L.append(f"  __shared__ __align__(16) mlc::f16 ks[{Tk * PK}];")
-    L.append(f"  __shared__ __align__(16) mlc::f16 vt[{D * PV}];")
-    L.append(f"  __shared__ __align__(16) mlc::f16 qs[{QB * PQ}];")
+    L.append(_type_aliases(k))
+    L.append(f"  __shared__ __align__(16) e16 ks[{Tk * PK}];")
+    L.append(f"  __shared__ __align__(16) e16 vt[{D * PV}];")
+    L.append(f"  __shared__ __align__(16) e16 qs[{QB * PQ}];")
     L += _tile_of_workgroup(BH, NQB, QB, it)
 
     ql_ = k.q.layout
@@ -237,18 +253,18 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     L.append("  const int qw = q0 + w * 16;")
     L.append(f"  if (qw >= {T}) return;  // no barrier follows")
     # scores
-    L.append(f"  mlc::half8 qf[{D // 32}];")
+    L.append(f"  v8 qf[{D // 32}];")
     L.append("#pragma unroll")
     L.append(f"  for (int dc = 0; dc < {D // 32}; ++dc)")
-    L.append(f"    qf[dc] = *reinterpret_cast<const mlc::half8*>(qs + (w * 16 + ql) * {PQ} + dc * 32 + g * 8);")
+    L.append(f"    qf[dc] = *reinterpret_cast<const v8*>(qs + (w * 16 + ql) * {PQ} + dc * 32 + g * 8);")
     L.append(f"  float s[{NT}][4];")
     L.append("#pragma unroll")
     L.append(f"  for (int t = 0; t < {NT}; ++t) {{")
     L.append("    mlc::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};")
     L.append("#pragma unroll")
     L.append(f"    for (int dc = 0; dc < {D // 32}; ++dc) {{")
-    L.append(f"      const mlc::half8 kf = *reinterpret_cast<const mlc::half8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
-    L.append("      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[dc], acc, 0, 0, 0);")
+    L.append(f"      const v8 kf = *reinterpret_cast<const v8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
+    L.append("      acc = mlc::mfma_16x16x32(kf, qf[dc], acc);")
     L.append("    }")
     L.append("#pragma unroll")
     L.append(f"    for (int i = 0; i < 4; ++i) s[t][i] = {cast_code('acc[i]', k.score_dtype)[0]};")
@@ -372,22 +388,22 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     L.append("#pragma unroll")
     L.append(f"  for (int dt = 0; dt < {D // 16}; ++dt) {{")
     L.append("    mlc::float4v o = {0.0f, 0.0f, 0.0f, 0.0f};")
-    L.append(f"    const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
+    L.append(f"    const e16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
     L.append("#pragma unroll")
     L.append(f"    for (int m = 0; m < {NT // 2}; ++m) {{")
-    L.append("      const mlc::half8 a = *reinterpret_cast<const mlc::half8*>(vrow + m * 32);")
-    L.append("      const mlc::half8 b = {(mlc::f16)pr[2 * m][0], (mlc::f16)pr[2 * m][1], "
-             "(mlc::f16)pr[2 * m][2], (mlc::f16)pr[2 * m][3], (mlc::f16)pr[2 * m + 1][0], "
-             "(mlc::f16)pr[2 * m + 1][1], (mlc::f16)pr[2 * m + 1][2], (mlc::f16)pr[2 * m + 1][3]};")
-    L.append("      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o, 0, 0, 0);")
+    L.append("      const v8 a = *reinterpret_cast<const v8*>(vrow + m * 32);")
+    L.append("      const v8 b = {(e16)pr[2 * m][0], (e16)pr[2 * m][1], "
+             "(e16)pr[2 * m][2], (e16)pr[2 * m][3], (e16)pr[2 * m + 1][0], "
+             "(e16)pr[2 * m + 1][1], (e16)pr[2 * m + 1][2], (e16)pr[2 * m + 1][3]};")
+    L.append("      o = mlc::mfma_16x16x32(a, b, o);")
     L.append("    }")
     omap = k.outputs[0].index
     parts = render_terms(axis_terms(omap, "idx"), BH * T * D, "f0", it)
     if omap.base:
         parts.append(f"({it}){omap.base}")
-    L.append(f"    const mlc::half4 h = {{(mlc::f16)o[0], (mlc::f16)o[1], (mlc::f16)o[2], (mlc::f16)o[3]}};")
+    L.append(f"    const v4 h = {{(e16)o[0], (e16)o[1], (e16)o[2], (e16)o[3]}};")
     L.append(f"    const {it} f0 = row * ({it}){D} + ({it})(dt * 16 + g * 4);")
-    L.append(f"    *reinterpret_cast<mlc::half4*>(out0 + {join_offset(parts, it)}) = h;")
+    L.append(f"    *reinterpret_cast<v4*>(out0 + {join_offset(parts, it)}) = h;")
     L.append("  }")
     L.append("}")
     spec = LaunchSpec("", BH * NQB, THREADS, lds_bytes,
@@ -468,9 +484,10 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
              f"{KB} keys; {QB} queries per workgroup, 16 per wave; online softmax")
     if FAST_SOFTMAX_MATH:
         L.append("#pragma clang fp contract(fast)")
-    L.append(f"  __shared__ __align__(16) mlc::f16 ks[{KB * PK}];")
-    L.append(f"  __shared__ __align__(16) mlc::f16 vt[{D * PV}];")
-    L.append(f"  __shared__ __align__(16) mlc::f16 qs[{QB * PQ}];")
+    L.append(_type_aliases(k))
+    L.append(f"  __shared__ __align__(16) e16 ks[{KB * PK}];")
+    L.append(f"  __shared__ __align__(16) e16 vt[{D * PV}];")
+    L.append(f"  __shared__ __align__(16) e16 qs[{QB * PQ}];")
     L += _tile_of_workgroup(BH, NQB, QB, it)
     ql_ = k.q.layout
     qsb, qsr, qsc = ql_.strides
@@ -506,10 +523,10 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("  const int qw = q0 + w * 16;")
     L.append(f"  const bool active = qw < {T};  // wave-uniform; every wave meets every barrier")
     L.append(f"  const {it} row = bh * ({it}){T} + ({it})(active ? qw + ql : 0);")
-    L.append(f"  mlc::half8 qf[{D // 32}];")
+    L.append(f"  v8 qf[{D // 32}];")
     L.append("#pragma unroll")
     L.append(f"  for (int dc = 0; dc < {D // 32}; ++dc)")
-    L.append(f"    qf[dc] = *reinterpret_cast<const mlc::half8*>(qs + (w * 16 + ql) * {PQ} + dc * 32 + g * 8);")
+    L.append(f"    qf[dc] = *reinterpret_cast<const v8*>(qs + (w * 16 + ql) * {PQ} + dc * 32 + g * 8);")
     L.append("  float m_run = (-__builtin_huge_valf()), l_run = 0.0f;")
     L.append(f"  mlc::float4v o[{D // 16}];")
     L.append("#pragma unroll")
@@ -610,11 +627,11 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append(f"      for (int t = 0; t < {NT}; ++t) acc[t] = mlc::float4v{{0.0f, 0.0f, 0.0f, 0.0f}};")
     L.append("#pragma unroll")
     L.append(f"      for (int dc = 0; dc < {D // 32}; ++dc) {{")
-    L.append(f"        mlc::half8 kf[{NT}];")
+    L.append(f"        v8 kf[{NT}];")
     L.append("#pragma unroll")
-    L.append(f"        for (int t = 0; t < {NT}; ++t) kf[t] = *reinterpret_cast<const mlc::half8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
+    L.append(f"        for (int t = 0; t < {NT}; ++t) kf[t] = *reinterpret_cast<const v8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
     L.append("#pragma unroll")
-    L.append(f"        for (int t = 0; t < {NT}; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t], qf[dc], acc[t], 0, 0, 0);")
+    L.append(f"        for (int t = 0; t < {NT}; ++t) acc[t] = mlc::mfma_16x16x32(kf[t], qf[dc], acc[t]);")
     L.append("      }")
     L.append(f"      float s[{NT}][4];")
     L.append("#pragma unroll")
@@ -662,17 +679,17 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     if D <= 64:
         # the V^T operands do not depend on the probabilities: read them now,
         # so their LDS latency hides behind the exponentials
-        L.append(f"      mlc::half8 va[{D // 16}][{NT // 2}];")
+        L.append(f"      v8 va[{D // 16}][{NT // 2}];")
         L.append("#pragma unroll")
         L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt)")
         L.append("#pragma unroll")
         L.append(f"        for (int m = 0; m < {NT // 2}; ++m)")
-        L.append(f"          va[dt][m] = *reinterpret_cast<const mlc::half8*>(vt + (dt * 16 + ql) * {PV} + g * 8 + m * 32);  // keys vperm-ed")
+        L.append(f"          va[dt][m] = *reinterpret_cast<const v8*>(vt + (dt * 16 + ql) * {PV} + g * 8 + m * 32);  // keys vperm-ed")
     L.append("      const float m_new = mlc::max_<float>(m_run, mb);")
     L.append(f"      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : {exp_}(m_run - m_new);")
     L.append("      // a row with no finite score yet subtracts 0: its x are all -inf, exp gives 0")
     L.append("      const float m_sub = m_new == (-__builtin_huge_valf()) ? 0.0f : m_new;")
-    L.append(f"      mlc::half4 p[{NT}];")
+    L.append(f"      v4 p[{NT}];")
     L.append("      float psum = 0.0f;")
     L.append("#pragma unroll")
     L.append(f"      for (int t = 0; t < {NT}; ++t)")
@@ -680,14 +697,14 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("        for (int i = 0; i < 4; ++i) {")
     L.append(f"          const float e = {exp_}(x[t][i] - m_sub);")
     L.append("          psum += e;")
-    L.append(f"          p[t][i] = (mlc::f16)e;")
+    L.append(f"          p[t][i] = (e16)e;")
     L.append("        }")
     L.append("      l_run = l_run * alpha + psum;")
     L.append("      m_run = m_new;")
-    L.append(f"      mlc::half8 bq[{NT // 2}];")
+    L.append(f"      v8 bq[{NT // 2}];")
     L.append("#pragma unroll")
     L.append(f"      for (int m = 0; m < {NT // 2}; ++m)")
-    L.append("        bq[m] = mlc::half8{p[2 * m][0], p[2 * m][1], p[2 * m][2], p[2 * m][3], "
+    L.append("        bq[m] = v8{p[2 * m][0], p[2 * m][1], p[2 * m][2], p[2 * m][3], "
              "p[2 * m + 1][0], p[2 * m + 1][1], p[2 * m + 1][2], p[2 * m + 1][3]};")
     L.append("#pragma unroll")
     L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt) o[dt] *= alpha;")
@@ -698,15 +715,15 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
         L.append(f"      for (int m = 0; m < {NT // 2}; ++m)")
         L.append("#pragma unroll")
         L.append(f"        for (int dt = 0; dt < {D // 16}; ++dt)")
-        L.append("          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt][m], bq[m], o[dt], 0, 0, 0);")
+        L.append("          o[dt] = mlc::mfma_16x16x32(va[dt][m], bq[m], o[dt]);")
     else:
         L.append("#pragma unroll")
         L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt) {{")
-        L.append(f"        const mlc::f16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
+        L.append(f"        const e16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
         L.append("#pragma unroll")
         L.append(f"        for (int m = 0; m < {NT // 2}; ++m) {{")
-        L.append("          const mlc::half8 a = *reinterpret_cast<const mlc::half8*>(vrow + m * 32);")
-        L.append("          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[m], o[dt], 0, 0, 0);")
+        L.append("          const v8 a = *reinterpret_cast<const v8*>(vrow + m * 32);")
+        L.append("          o[dt] = mlc::mfma_16x16x32(a, bq[m], o[dt]);")
         L.append("        }")
         L.append("      }")
     L.append("      }")
@@ -729,10 +746,10 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
         parts.append(f"({it}){omap.base}")
     L.append("#pragma unroll")
     L.append(f"  for (int dt = 0; dt < {D // 16}; ++dt) {{")
-    L.append(f"    const mlc::half4 h = {{(mlc::f16)(o[dt][0] {div}), (mlc::f16)(o[dt][1] {div}), "
-             f"(mlc::f16)(o[dt][2] {div}), (mlc::f16)(o[dt][3] {div})}};")
+    L.append(f"    const v4 h = {{(e16)(o[dt][0] {div}), (e16)(o[dt][1] {div}), "
+             f"(e16)(o[dt][2] {div}), (e16)(o[dt][3] {div})}};")
     L.append(f"    const {it} f0 = row * ({it}){D} + ({it})(dt * 16 + g * 4);")
-    L.append(f"    *reinterpret_cast<mlc::half4*>(out0 + {join_offset(parts, it)}) = h;")
+    L.append(f"    *reinterpret_cast<v4*>(out0 + {join_offset(parts, it)}) = h;")
     L.append("  }")
     L.append("}")
     spec = LaunchSpec("", BH * NQB, THREADS, lds_bytes,

@@ -71,8 +71,19 @@ template <class S, class X> __device__ __forceinline__ void st(S* p, X x) { *p =
 // MFMA operand/accumulator fragments and a 16-byte bit copy of 8 halfs
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 struct alignas(16) f16x8 { f16 v[8]; };
+
+// One 16x16x32 MFMA step, D = A B + C with fp32 accumulation, for either
+// 16-bit operand type (the attention kernels are written once for both).
+__device__ __forceinline__ float4v mfma_16x16x32(half8 a, half8 b, float4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float4v mfma_16x16x32(bf16x8 a, bf16x8 b, float4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 
 // Key position inside a staged V^T row of the attention kernels: within each
 // 32-key chunk, key 16h + 4g + i sits at 8g + 4h + i, so the 8 keys one lane

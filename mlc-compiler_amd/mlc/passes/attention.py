@@ -13,8 +13,8 @@ Applies when the scores feed only the reduction, the reduction reads them at
 identity over a ``[BH*T] x [Tk]`` frame and writes only the probabilities,
 those feed only the second ``bmm`` as its first operand, scores,
 probabilities and output are contiguous, T is a multiple of 16, the head size
-a multiple of 32 up to 128, and the operands fp16 (the MFMA the kernel is
-built on). Up to 128 keys (a multiple of 32) every score of a row stays in
+a multiple of 32 up to 128, and the operands fp16 or bf16 (the 16-bit MFMAs
+the kernel is built on). Up to 128 keys (a multiple of 32) every score of a row stays in
 registers and the reduction's own steps are rendered, whatever they are.
 Longer rows (a multiple of 64 keys) are streamed in key blocks with the
 online-softmax recurrence, which needs the reduction to be exactly a softmax
@@ -252,7 +252,8 @@ def _match(kernels, i, readers, graph_outputs):
     elif Tk % 32:
         return None
     dt = q.dtype
-    if dt != torch.float16 or any(x.dtype != dt for x in (kt, v, o_val, s_val, prob)):
+    if dt not in (torch.float16, torch.bfloat16) or \
+            any(x.dtype != dt for x in (kt, v, o_val, s_val, prob)):
         return None
     for x in (s_val, p_val, o_val):
         if not (x.layout.is_contiguous() and x.layout.offset == 0):

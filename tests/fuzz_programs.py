@@ -278,13 +278,13 @@ def max_rel_error(got: torch.Tensor, want: torch.Tensor) -> float:
     return (g - w).abs().max().item() / scale
 
 
-def attention_case(seed: int):
+def attention_case(seed: int, dtype=torch.float16):
     """A random attention problem for the fused kernels: (model, inputs,
     description). Queries in multiples of 16; up to 128 keys in multiples of
     32 (single pass) or 192..640 in multiples of 64 (key-blocked); head sizes
     32..128; one of five masks: padding at -10000 or -inf, causal (-inf, every
     row keeps its diagonal), a per-head additive bias, or zeros. Scaled by a
-    division or a multiplication."""
+    division or a multiplication. ``dtype`` is fp16 or bf16."""
     import math
 
     rng = random.Random(1000 + seed)
@@ -295,21 +295,21 @@ def attention_case(seed: int):
     kind = rng.choice(["padding", "padding_inf", "causal", "bias", "zeros"])
     by_div = rng.random() < 0.5
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn(b, h, t, d, generator=g).half()
-    k = torch.randn(b, h, tk, d, generator=g).half()
-    v = torch.randn(b, h, tk, d, generator=g).half()
+    q = torch.randn(b, h, t, d, generator=g).to(dtype)
+    k = torch.randn(b, h, tk, d, generator=g).to(dtype)
+    v = torch.randn(b, h, tk, d, generator=g).to(dtype)
     if kind in ("padding", "padding_inf"):
         keep = torch.rand(b, 1, 1, tk, generator=g) >= 0.2
         keep[..., 0] = True
         fill = -10000.0 if kind == "padding" else float("-inf")
-        mask = torch.where(keep, 0.0, fill).half()
+        mask = torch.where(keep, 0.0, fill).to(dtype)
     elif kind == "causal":
         mask = torch.triu(torch.full((t, tk), float("-inf")), diagonal=1 + max(0, tk - t))
-        mask = mask.half()[None, None]
+        mask = mask.to(dtype)[None, None]
     elif kind == "bias":
-        mask = torch.randn(1, h, t, tk, generator=g).half()
+        mask = torch.randn(1, h, t, tk, generator=g).to(dtype)
     else:
-        mask = torch.zeros(b, 1, 1, tk).half()
+        mask = torch.zeros(b, 1, 1, tk).to(dtype)
 
     class Attn(torch.nn.Module):
         def forward(self, q, k, v, mask):
@@ -317,7 +317,8 @@ def attention_case(seed: int):
             s = s / math.sqrt(d) if by_div else s * (1.0 / math.sqrt(d))
             return (s + mask).softmax(dim=-1) @ v
 
-    desc = f"b{b} h{h} T{t} Tk{tk} d{d} {kind} {'div' if by_div else 'mul'}"
+    desc = (f"b{b} h{h} T{t} Tk{tk} d{d} {kind} {'div' if by_div else 'mul'}"
+            + ("" if dtype == torch.float16 else f" {str(dtype)[6:]}"))
     return Attn(), (q, k, v, mask), desc
 
 

@@ -92,6 +92,8 @@ def test_refused_when_scores_escape_or_shapes_do_not_fit():
     assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 1
     q, k, v, m = _inputs(1, 2, 32, 32, 64, torch.float32)
     assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
+    q, k, v, m = _inputs(1, 2, 32, 32, 64, torch.bfloat16)  # the bf16 MFMA takes these
+    assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 1
     q, k, v, m = _inputs(1, 2, 32, 48, 64)  # keys not a multiple of 32
     assert len(_attention(build_pipeline(capture(Attention(), (q, k, v, m)), ATTN))) == 0
     q, k, v, m = _inputs(1, 2, 32, 32, 48)  # head size not a multiple of 32
@@ -120,6 +122,39 @@ def test_oracle_fused_attention_matches_float64(shape):
     assert err <= max(2e-3, 2 * err_unfused)
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 32, 32, 64), (1, 2, 80, 96, 32), (1, 2, 48, 256, 64),
+                                   (2, 1, 16, 192, 128)])
+def test_oracle_bf16_fused_attention_matches_float64(shape):
+    """The same check in bf16 (8 significand bits, so the bar is wider):
+    within 1.5e-2 of the largest output and within twice the unfused
+    schedule's error."""
+    args = _inputs(*shape, dtype=torch.bfloat16, seed=3)
+    model = Attention()
+    sched = build_pipeline(capture(model, args), ATTN)
+    assert [a.q.dtype for a in _attention(sched)] == [torch.bfloat16]
+    got = compile_reference(model, args, ATTN)(*args)
+    unfused = compile_reference(model, args, Config(cuda_graphs=False))(*args)
+    exact = model(*(a.double() for a in args))
+    scale = exact.abs().max().item()
+    err = (got.double() - exact).abs().max().item() / scale
+    err_unfused = (unfused.double() - exact).abs().max().item() / scale
+    assert err <= 1.5e-2
+    assert err <= max(1.5e-2, 2 * err_unfused)
+
+
+def test_bf16_kernels_bind_the_bf16_types():
+    """The emitter writes one kernel text over ``e16``/``v8``/``v4``; a bf16
+    head binds them to ``__bf16`` vectors, whose ``mlc::mfma_16x16x32``
+    overload is the bf16 MFMA."""
+    for shape in ((2, 3, 32, 32, 64), (1, 2, 48, 256, 64)):
+        args = _inputs(*shape, dtype=torch.bfloat16)
+        sched = build_pipeline(capture(Attention(), args), ATTN)
+        mod = generate_module(sched, ATTN)
+        body = mod.functions[mod.launches[_attention(sched)[0].name].symbol]
+        assert "using e16 = __bf16;" in body and "using v8 = mlc::bf16x8;" in body
+        assert "mlc::f16" not in body and "half" not in body
+
+
 def test_oracle_fused_models_match_unfused():
     for name in ("bert-small", "gpt-small"):
         model, args = build(name, 2, 32, "cpu", torch.float16)
@@ -140,16 +175,17 @@ def test_generated_kernel_shape():
     assert spec.block == 128 and spec.grid == 12 * 4
     assert spec.lds_bytes <= 64 * 1024
     body = mod.functions[spec.symbol]
-    assert body.count("__builtin_amdgcn_mfma_f32_16x16x32_f16") == 2
+    assert body.count("mlc::mfma_16x16x32(") == 2 and "using e16 = mlc::f16;" in body
     assert "__syncthreads();" in body and body.index("__syncthreads();") < body.index("return;")
     # C2's merged-qkv views are unit-stride along the head dim: 128-bit LDS stores
-    assert body.count("*reinterpret_cast<mlc::half8*>(") == 2
+    assert body.count("*reinterpret_cast<v8*>(") == 2
 
 
 def test_attention_module_cross_compiles_for_gfx950(tmp_path, monkeypatch):
     monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
-    for shape in ((1, 2, 80, 96, 32), (2, 3, 32, 32, 64)):
-        args = _inputs(*shape)
+    for shape, dt in (((1, 2, 80, 96, 32), torch.float16), ((2, 3, 32, 32, 64), torch.float16),
+                      ((1, 2, 48, 256, 64), torch.bfloat16)):
+        args = _inputs(*shape, dtype=dt)
         sched = build_pipeline(capture(Attention(), args), ATTN)
         mod = generate_module(sched, ATTN)
         _, obj = native.compile_code_object(mod.source)
@@ -168,9 +204,9 @@ def test_operand_producers_write_the_mfma_layouts():
         body = mod.functions[mod.launches[a.name].symbol]
         # Q and K: one 128-bit store per pack; V^T: two 64-bit stores at the
         # key-permuted positions the 128-bit MFMA-operand reads expect
-        assert body.count("*reinterpret_cast<mlc::half8*>(") == 2 and "[u][j]" not in body
-        assert body.count("*reinterpret_cast<mlc::half4*>(vt + mlc::vperm(") == 2
-        assert body.count("*reinterpret_cast<const mlc::half8*>(vrow") == 1
+        assert body.count("*reinterpret_cast<v8*>(") == 2 and "[u][j]" not in body
+        assert body.count("*reinterpret_cast<v4*>(vt + mlc::vperm(") == 2
+        assert body.count("*reinterpret_cast<const v8*>(vrow") == 1
     assert not verify(list(sched.plan.live_ranges.values()), sched.plan.offsets)
 
 

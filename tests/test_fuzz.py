@@ -214,6 +214,50 @@ def test_random_attention_hip_matches_oracle(seed):
     assert e_oracle <= 2e-3 and e_exact <= 2e-3, desc
 
 
+# bf16 keeps 8 significand bits (unit roundoff 2^-9). Against float64 the
+# program itself rounds the scores, the probabilities and the output to bf16
+# (a score near 4 moves by up to 2^-7, its probability by 0.8%), so that bar
+# is about six ulps of the largest output; the HIP kernel and the oracle
+# round the same values and differ only in summation order and exp, so that
+# bar is tighter.
+BF16_ATTN_BAR = 2.5e-2
+BF16_ORACLE_BAR = 1e-2
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_bf16_attention_oracle_matches_float64(seed):
+    """bf16 attention problems fuse too; the oracle's fused kernel is within
+    the bf16 bar of float64 attention."""
+    from mlc.kernels import AttentionKernel
+
+    model, args, desc = fp.attention_case(seed, torch.bfloat16)
+    sched = build_pipeline(capture(model, args), ATTN)
+    assert sum(isinstance(k, AttentionKernel) for k in sched.kernels) == 1, desc
+    got = compile_reference(model, args, ATTN)(*args)
+    assert torch.isfinite(got).all() and _fp64_err(got, model, args) <= BF16_ATTN_BAR, desc
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(16))
+def test_random_bf16_attention_hip_matches_oracle(seed):
+    """The bf16 MFMA attention kernels on random problems: within the bf16
+    bars of the oracle's fused kernel and of float64."""
+    import mlc
+
+    model, args, desc = fp.attention_case(seed, torch.bfloat16)
+    want = compile_reference(model, args, ATTN)(*args)
+    dev = tuple(a.cuda() for a in args)
+    print(desc, flush=True)
+    compiled = mlc.compile(model, dev, ATTN)
+    assert [s.meta["kind"] for s in compiled._module.launch_table.values()].count("attention") == 1
+    got = compiled(*dev)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16 and torch.isfinite(got).all(), desc
+    e_oracle, e_exact = fp.max_rel_error(got.cpu(), want), _fp64_err(got, model, args)
+    print(f"  hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}", flush=True)
+    assert e_oracle <= BF16_ORACLE_BAR and e_exact <= BF16_ATTN_BAR, desc
+
+
 EVERY = Config(cuda_graphs=False, merge_parallel_gemms=True, gemm_epilogue=True,
                layout_selection=True, fused_attention=True)
 

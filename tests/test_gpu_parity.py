@@ -21,6 +21,7 @@ import torch
 import mlc
 from gpu_util import flat_outputs, lockstep, rel_err
 from mlc.api import build_pipeline
+from mlc.bench.models import build
 from mlc.bench.workloads import make
 from mlc.config import Config
 from mlc.ir.capture import capture
@@ -477,6 +478,50 @@ def test_fused_attention_shapes(shape):
     e_oracle, e_exact = rel_err(got, want), rel_err(got, exact)
     print(shape, f"hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}")
     assert e_oracle <= 2e-3 and e_exact <= 2e-3
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 32, 32, 64), (1, 2, 80, 96, 32), (1, 1, 16, 128, 128),
+                                   (1, 2, 48, 256, 64), (1, 1, 80, 320, 128)],
+                         ids=["b2h3-32x32-d64", "80x96-d32-partial-block", "16x128-d128",
+                              "48x256-key-blocked", "80x320-d128-key-blocked-partial"])
+def test_fused_attention_shapes_bf16(shape):
+    """The same kernels with bf16 operands (the bf16 MFMA, bf16 scores and
+    probabilities): within 1e-2 of the oracle's fused kernel and 2.5e-2 of
+    float64 attention, a few bf16 ulps of the largest output."""
+    from test_attention import Attention, _inputs
+
+    args = _inputs(*shape, dtype=torch.bfloat16)
+    model = Attention()
+    want = compile_reference(model, args, Config(fused_attention=True, cuda_graphs=False))(*args)
+    exact = model(*(a.double() for a in args))
+    compiled = mlc.compile(model, tuple(a.cuda() for a in args), ATTN)
+    kinds = [s.meta["kind"] for s in compiled._module.launch_table.values()]
+    assert kinds.count("attention") == 1
+    got = compiled(*(a.cuda() for a in args))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16
+    e_oracle, e_exact = rel_err(got, want), rel_err(got, exact)
+    print(shape, f"hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}")
+    assert e_oracle <= 1e-2 and e_exact <= 2.5e-2
+
+
+@pytest.mark.parametrize("name", ["bert-small", "gpt-small"])
+def test_bf16_models_with_fused_attention(name):
+    """Whole bf16 models (every pointwise, reduction and attention kernel in
+    bf16, GEMMs in PyTorch) with fused attention against the oracle running
+    the same schedule: within 3e-2 of the largest output, bf16's bar for a
+    multi-layer program."""
+    model, args = build(name, 2, 32, "cpu", torch.bfloat16)
+    cfg = Config(fused_attention=True, cuda_graphs=False)
+    want = compile_reference(model, args, cfg)(*args)
+    model, dev = model.cuda(), tuple(a.cuda() for a in args)
+    compiled = mlc.compile(model, dev, ATTN)
+    assert compiled.schedule.counts()["attention"] == 4
+    got = compiled(*dev)
+    torch.cuda.synchronize()
+    err = rel_err(got, want)
+    print(name, f"bf16 hip-vs-oracle {err:.2e}")
+    assert torch.isfinite(got.float()).all() and err <= 3e-2
 
 
 @pytest.mark.parametrize("key", ["C2", "C3"])
