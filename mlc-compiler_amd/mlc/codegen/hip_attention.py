@@ -61,6 +61,10 @@ FAST_SOFTMAX_MATH = True
 #: 8); 384 heads -> 8 waves (12.6 us vs 14.8 at 4, 18.3 at 2).
 ATTENTION_TUNING = {"waves": None, "choices": (8, 4, 2), "min_workgroups": 256}
 
+#: halfs of padding after each LDS row of Q, K and V^T (a multiple of 8, so
+#: every row starts 16-byte aligned for the 128-bit operand reads)
+LDS_ROW_PAD = 8
+
 
 def attention_waves(heads: int, queries: int) -> int:
     forced = ATTENTION_TUNING["waves"]
@@ -208,7 +212,7 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     NQB = -(-T // QB)
     THREADS = W * WAVE
     it = index_type(k)
-    PK, PV, PQ = D + 8, Tk + 8, D + 8
+    PK, PV, PQ = D + LDS_ROW_PAD, Tk + LDS_ROW_PAD, D + LDS_ROW_PAD
     lds_bytes = 2 * (Tk * PK + D * PV + QB * PQ)
 
     L: list[str] = []
@@ -474,7 +478,7 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     NQB = -(-T // QB)
     THREADS = W * WAVE
     it = index_type(k)
-    PK, PV, PQ = D + 8, KB + 8, D + 8
+    PK, PV, PQ = D + LDS_ROW_PAD, KB + LDS_ROW_PAD, D + LDS_ROW_PAD
     lds_bytes = 2 * (KB * PK + D * PV + QB * PQ)
 
     L: list[str] = []
