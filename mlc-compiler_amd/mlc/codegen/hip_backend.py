@@ -686,7 +686,10 @@ def reduction_geometry(n_rows: int, n_cols: int, V: int) -> dict:
         G = 128
         while G < 1024 and -(-nvec // G) > t["max_packs"]:
             G *= 2
-    K = -(-nvec // G)
+    # at least one pack: rows of zero columns (an empty reduced dim) keep
+    # their one pack, every lane of it out of range, so each row reduces to
+    # the identity and no column is loaded or stored
+    K = max(1, -(-nvec // G))
     if G <= WAVE:
         cap = max(1, t["block"] // G)
         rows = max(WAVE // G, min(cap, max(1, -(-n_rows // 1024))))

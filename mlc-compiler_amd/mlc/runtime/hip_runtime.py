@@ -158,6 +158,8 @@ class HipRuntime:
         self.run_bound(self.bind(k, buffers))
 
     def run_bound(self, payload) -> None:
+        if isinstance(payload, Bound) and payload.grid == 0:
+            return  # a reduction over zero rows: nothing to launch
         if isinstance(payload, Range):
             native.check(self.lib.mlc_plan_run(payload.plan, payload.begin, payload.end, _stream()),
                          "mlc_plan_run")
@@ -172,7 +174,7 @@ class HipRuntime:
         generated kernels is one ``Range`` of a native launch plan."""
         def native_of(kind, payload):
             if kind == "kernel":
-                return payload
+                return payload if payload.grid else None
             if kind == "extern" and payload[0] == "native" and payload[1] is self:
                 return payload[2]
             return None
@@ -236,6 +238,8 @@ class HipRuntime:
     def time_bound(self, payload: Bound, iters: int, stream: int) -> float:
         """Average ms of ``iters`` back-to-back launches of one bound kernel,
         timed with hipEvents on ``stream``."""
+        if payload.grid == 0:
+            return 0.0
         handle = ctypes.c_void_p()
         native.check(self.lib.mlc_plan_create(self._ctx, 1, ctypes.byref(handle)), "mlc_plan_create")
         try:

@@ -6,7 +6,8 @@ Each case is a small program at the edge of the reduction-fusion frame rules:
 a row output that reads a row-constant operand, a reshape of the row shape,
 shapes that right-align onto the element shape (among them a LayerNorm whose
 batch is 1 and whose rows are as long as the sequence), a permutation that
-passes the reshape test. Per case the fixture records what the reference does:
+passes the reshape test, and zero-element inputs (no rows, or rows of no
+columns). Per case the fixture records what the reference does:
 the exception it raises (type and message), or its schedule (kernel
 summaries, operand buffers and index strings) and whether its torch backend's
 outputs agree with eager PyTorch (or the error its torch backend raises). Nothing else pins the front end there: the
@@ -54,6 +55,18 @@ def cases():
         def forward(self, x):
             return F.layer_norm(x, (x.shape[-1],))
 
+    class AffineRelu(torch.nn.Module):
+        def forward(self, x):
+            return torch.relu(x * 2.0 + 1.0)
+
+    class Softmax(torch.nn.Module):
+        def forward(self, x):
+            return torch.softmax(x, dim=-1)
+
+    class RowSum(torch.nn.Module):
+        def forward(self, x):
+            return x.sum(dim=-1)
+
     g = torch.Generator().manual_seed(0)
 
     def rn(*s, dt=torch.float32):
@@ -69,6 +82,13 @@ def cases():
         ("permuted_row_value", PermutedRowValue(), (rn(16, 3, 64, 5), rn(3, 64, 1))),
         ("layer_norm_row_matches_trailing", LayerNormRowMatchesTrailing(), (rn(1, 128, 128),)),
         ("layer_norm_b2", LayerNormRowMatchesTrailing(), (rn(2, 128, 128),)),
+        # zero-element inputs: no rows, or rows of no columns
+        ("empty_rows_pointwise", AffineRelu(), (rn(0, 16),)),
+        ("empty_rows_softmax", Softmax(), (rn(0, 16),)),
+        ("empty_rows_sum", RowSum(), (rn(0, 16),)),
+        ("empty_rows_layer_norm", LayerNormRowMatchesTrailing(), (rn(0, 16),)),
+        ("empty_cols_sum", RowSum(), (rn(4, 0),)),
+        ("empty_cols_softmax", Softmax(), (rn(4, 0),)),
     ]
 
 

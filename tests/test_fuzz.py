@@ -123,6 +123,73 @@ def test_edge_case_permuted_producer_is_not_fused():
     torch.testing.assert_close(got, model(*args), rtol=1e-5, atol=1e-5)
 
 
+EMPTY = ["empty_rows_pointwise", "empty_rows_softmax", "empty_rows_sum", "empty_cols_sum",
+         "empty_cols_softmax"]
+
+
+@pytest.mark.parametrize("name", EMPTY)
+def test_empty_inputs_compile_like_the_reference(name):
+    """Zero-element inputs (no rows, or rows of no columns) compile to the
+    reference's kernels (recorded summaries, and its torch backend matched
+    eager), and the oracle returns eager's result: empty, or zeros for a sum
+    over an empty dim."""
+    model, args = _case(name)
+    rec = FIXTURE[name]
+    assert rec["matches_eager"] is True
+    sched = build_pipeline(capture(model, args), CFG)
+    assert [k.summary() for k in sched.kernels] == [k["summary"] for k in rec["kernels"]]
+    got = compile_reference(model, args, CFG)(*args)
+    want = model(*args)
+    assert got.shape == want.shape and got.dtype == want.dtype and torch.equal(got, want)
+
+
+def test_empty_rows_layer_norm_raises_like_the_reference():
+    """LayerNorm over zero rows: capture raises the reference's own error
+    (type and message recorded)."""
+    model, args = _case("empty_rows_layer_norm")
+    with pytest.raises(Exception) as err:
+        build_pipeline(capture(model, args), CFG)
+    assert [type(err.value).__name__, str(err.value)] == FIXTURE["empty_rows_layer_norm"]["error"]
+
+
+def test_empty_reductions_launch_nothing_or_one_idle_pack(tmp_path, monkeypatch):
+    """Zero rows: a grid of 0 workgroups, which the runtime does not launch.
+    Zero columns: one pack per row whose lanes are all out of range, so a row
+    reduces to the identity without a load (a zero-length pack array would
+    not compile for the device)."""
+    from mlc.codegen.hip_backend import generate_module
+    from mlc.runtime import native
+
+    monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
+    for name, grid in (("empty_rows_sum", 0), ("empty_cols_sum", 1)):
+        model, args = _case(name)
+        sched = build_pipeline(capture(model, args), CFG)
+        mod = generate_module(sched, CFG)
+        spec = mod.launches[sched.kernels[0].name]
+        assert spec.grid == grid
+    assert spec.meta["packs"] == 1 and "valid[p] =" in mod.functions[spec.symbol]
+    _, obj = native.compile_code_object(mod.source)
+    assert obj.stat().st_size > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("graphs", [False, True], ids=["plan", "graph"])
+@pytest.mark.parametrize("name", EMPTY)
+def test_empty_inputs_on_the_gpu(name, graphs):
+    """The same programs on the GPU, planned and captured: eager's result
+    exactly."""
+    import mlc
+
+    model, args = _case(name)
+    want = model(*args)
+    dev = tuple(a.cuda() for a in args)
+    print(name, "graphs" if graphs else "plan", flush=True)
+    got = mlc.compile(model, dev, Config(cuda_graphs=graphs))(*dev)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape and got.dtype == want.dtype
+    assert torch.equal(got.cpu(), want)
+
+
 GPU_CASES = [(s, "default") for s in range(16)] + [(s, "streamed") for s in range(6)] + \
     [(s, "layout") for s in range(4)] + [(s, "wide") for s in range(6)] + \
     [(s, "wide_streamed") for s in range(3)] + [(s, "no_fusion") for s in range(2)] + \
