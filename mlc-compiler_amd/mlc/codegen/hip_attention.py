@@ -9,10 +9,11 @@ queries):
   are copied from their strided views into LDS with 128-bit loads along
   whichever axis is unit-stride, all loads issued before the first LDS
   store. K is kept as ``[key][d]`` and V transposed
-  as ``[d][key]``; row pitches are padded by 8 halfs so the 16-lane phases of
-  ``ds_read_b128`` hit distinct banks.
+  as ``[d][key]``; row pitches are padded by 8 elements so the 16-lane phases
+  of ``ds_read_b128`` hit distinct banks.
 * **scores**: each wave owns 16 queries and computes ``S^T = K Q^T`` with
-  ``v_mfma_f32_16x16x32_f16`` -- A = a 16-key tile of K, B = the wave's Q
+  ``v_mfma_f32_16x16x32_f16`` (``_bf16`` for bf16 heads; the body is written
+  once over the ``e16``/``v8``/``v4`` aliases) -- A = a 16-key tile of K, B = the wave's Q
   fragment (read once) -- so lane ``l`` ends up holding query ``l % 16``'s
   scores for keys ``16 t + 4 (l / 16) + i``. Scores are rounded to their
   storage dtype, as the unfused schedule stores them.
@@ -32,7 +33,8 @@ Numerics follow the unfused schedule: fp32 accumulation, scores and
 probabilities rounded to their storage dtypes before use, fp32 softmax.
 Summation orders differ from the library GEMMs and from the standalone
 reduction kernel, and the softmax's exp and division take fast forms
-(``FAST_SOFTMAX_MATH``), so results agree to fp16 rounding, not bit for bit.
+(``FAST_SOFTMAX_MATH``), so results agree to the operands' 16-bit rounding,
+not bit for bit.
 """
 
 from __future__ import annotations
@@ -49,9 +51,10 @@ from .reduction_schedule import varies_by_column
 #: the softmax's exp and its division by the row sum in fast forms
 #: (``mlc::exp_fast`` and a multiply by the row reciprocal), and floating-point
 #: contraction inside the attention kernels (a scale and a mask add become one
-#: mixed-precision FMA on the fp16 operands). All of it is used only here, where
-#: every probability is rounded to fp16 before it is used: the errors (about
-#: 1e-6, 1.5 fp32 ulp, one fp32 rounding) are far below that rounding.
+#: mixed-precision FMA on the 16-bit operands). All of it is used only here,
+#: where every probability is rounded to fp16 or bf16 before it is used: the
+#: errors (about 1e-6, 1.5 fp32 ulp, one fp32 rounding) are far below that
+#: rounding.
 FAST_SOFTMAX_MATH = True
 
 #: waves per workgroup (each owns 16 queries): ``waves`` forces a count;
