@@ -12,8 +12,8 @@ import pytest
 import torch
 
 from mlc.api import build_pipeline
-from mlc.codegen.hip_backend import (classify_access, emit_kernel, float_literal,
-                                     generate_module, reduction_geometry)
+from mlc.codegen.hip_backend import (classify_access, float_literal, generate_module,
+                                     reduction_geometry)
 from mlc.codegen.index import build_index, flat_index
 from mlc.config import Config
 from mlc.ir.capture import capture
