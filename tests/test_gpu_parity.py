@@ -524,6 +524,29 @@ def test_bf16_models_with_fused_attention(name):
     assert torch.isfinite(got.float()).all() and err <= 3e-2
 
 
+@pytest.mark.parametrize("name,batch", [("bert-base", 32), ("gpt2-small", 1)])
+def test_bf16_full_size_models_every_variant(name, batch):
+    """BERT-base b32 and GPT-2 small b1 at s128 in bf16 with every schedule
+    variant on (bf16 attention in all 12 layers) against the oracle running
+    the same schedule: within bf16's 3e-2 of the largest output. The
+    variants' oracle is itself about 1.4e-2 (BERT) from the reference
+    schedule's in bf16."""
+    cfg = Config(merge_parallel_gemms=True, gemm_epilogue=True, layout_selection=True,
+                 fused_attention=True)
+    model, args = build(name, batch, 128, "cpu", torch.bfloat16)
+    want = compile_reference(model, args, Config(merge_parallel_gemms=True, gemm_epilogue=True,
+                                                 layout_selection=True, fused_attention=True,
+                                                 cuda_graphs=False))(*args)
+    model, dev = model.cuda(), tuple(a.cuda() for a in args)
+    compiled = mlc.compile(model, dev, cfg)
+    assert compiled.schedule.counts()["attention"] == 12
+    got = compiled(*dev)
+    torch.cuda.synchronize()
+    err = rel_err(got, want)
+    print(name, f"b{batch} bf16 every variant: hip-vs-oracle {err:.2e}")
+    assert torch.isfinite(got.float()).all() and err <= 3e-2
+
+
 @pytest.mark.parametrize("key", ["C2", "C3"])
 def test_fused_attention_matches_reference_schedule(key):
     """The fused-attention schedule computes the same function as the
