@@ -29,6 +29,11 @@
  *   mlc_time_entry
  *       mlc/runtime/executor.py:309-352 (profile_kernels: CUDA-event timing of
  *       one plan entry in place), here with hipEvents on the launch stream.
+ *   mlc_error_word / mlc_error_fetch / mlc_error_poll / mlc_error_clear
+ *       the IndexError torch raises from aten.embedding for an id outside
+ *       the table (mlc/runtime/executor.py:369-402 sends the op to torch):
+ *       the native gather flags it in a device word instead, and the host
+ *       reads the word's pinned mirror without stalling the stream.
  *   mlc_last_error
  *       the Python exceptions of the reference (ExecutionError etc.).
  */
@@ -93,6 +98,18 @@ int mlc_graph_node_count(mlc_ctx* ctx, size_t* out);
 /* Average milliseconds of `iters` back-to-back launches of plan entry `index`
  * on `stream`, measured with hipEvents recorded on that stream. */
 int mlc_time_entry(mlc_plan* plan, int index, int iters, void* stream, float* ms_out);
+
+/* The context's invalid-input word (16 bytes of device memory, zeroed when
+ * first requested, with a pinned host mirror). Kernels that meet an invalid
+ * input (an embedding id outside its table) store a non-zero value in it. */
+int mlc_error_word(mlc_ctx* ctx, void** device_word);
+/* Enqueue an asynchronous copy of the word to its host mirror on `stream`
+ * (may be captured into a graph). */
+int mlc_error_fetch(mlc_ctx* ctx, void* stream);
+/* The host mirror's first int as of the last completed fetch; no sync. */
+int mlc_error_poll(mlc_ctx* ctx, int32_t* value);
+/* Synchronize the device, then zero the word and its mirror. */
+int mlc_error_clear(mlc_ctx* ctx);
 
 /* Synchronize the context's device. */
 int mlc_device_synchronize(mlc_ctx* ctx);

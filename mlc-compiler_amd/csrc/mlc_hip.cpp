@@ -63,6 +63,8 @@ struct DLManagedTensor {
 constexpr int32_t kDLROCM = 10;
 constexpr uint8_t kDLUInt = 1;
 
+constexpr size_t kErrorWordBytes = 16;
+
 struct Slab {
   void* ptr = nullptr;
   size_t bytes = 0;
@@ -122,6 +124,10 @@ struct mlc_ctx {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   hipStream_t capturing = nullptr;
+  // invalid-input word: set by kernels on the device, mirrored into pinned
+  // host memory by an asynchronous copy the caller enqueues after its work
+  int32_t* err_dev = nullptr;
+  volatile int32_t* err_host = nullptr;
 };
 
 struct mlc_module {
@@ -159,6 +165,8 @@ int mlc_ctx_destroy(mlc_ctx* ctx) {
   if (ctx->exec != nullptr) (void)hipGraphExecDestroy(ctx->exec);
   if (ctx->graph != nullptr) (void)hipGraphDestroy(ctx->graph);
   slab_release(ctx->slab);
+  if (ctx->err_dev != nullptr) (void)hipFree(ctx->err_dev);
+  if (ctx->err_host != nullptr) (void)hipHostFree(const_cast<int32_t*>(ctx->err_host));
   delete ctx;
   return MLC_OK;
 }
@@ -377,6 +385,52 @@ int mlc_time_entry(mlc_plan* plan, int index, int iters, void* stream, float* ms
   if (rc != MLC_OK) return rc;
   if (err != hipSuccess) return hip_fail(err, "mlc_time_entry");
   *ms_out = ms / static_cast<float>(iters);
+  return MLC_OK;
+}
+
+int mlc_error_word(mlc_ctx* ctx, void** device_word) {
+  if (ctx == nullptr || device_word == nullptr) return fail(MLC_E_ARG, "mlc_error_word: bad argument");
+  if (ctx->err_dev == nullptr) {
+    MLC_HIP(hipSetDevice(ctx->device));
+    void* d = nullptr;
+    void* h = nullptr;
+    MLC_HIP(hipMalloc(&d, kErrorWordBytes));
+    hipError_t e = hipHostMalloc(&h, kErrorWordBytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMemset(d, 0, kErrorWordBytes);
+    if (e != hipSuccess) {
+      (void)hipFree(d);
+      if (h != nullptr) (void)hipHostFree(h);
+      return hip_fail(e, "mlc_error_word");
+    }
+    std::memset(h, 0, kErrorWordBytes);
+    ctx->err_dev = static_cast<int32_t*>(d);
+    ctx->err_host = static_cast<volatile int32_t*>(h);
+  }
+  *device_word = ctx->err_dev;
+  return MLC_OK;
+}
+
+int mlc_error_fetch(mlc_ctx* ctx, void* stream) {
+  if (ctx == nullptr) return fail(MLC_E_ARG, "mlc_error_fetch: null ctx");
+  if (ctx->err_dev == nullptr) return fail(MLC_E_STATE, "mlc_error_fetch: no error word");
+  MLC_HIP(hipMemcpyAsync(const_cast<int32_t*>(ctx->err_host), ctx->err_dev, kErrorWordBytes,
+                         hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream)));
+  return MLC_OK;
+}
+
+int mlc_error_poll(mlc_ctx* ctx, int32_t* value) {
+  if (ctx == nullptr || value == nullptr) return fail(MLC_E_ARG, "mlc_error_poll: bad argument");
+  *value = ctx->err_host == nullptr ? 0 : ctx->err_host[0];
+  return MLC_OK;
+}
+
+int mlc_error_clear(mlc_ctx* ctx) {
+  if (ctx == nullptr) return fail(MLC_E_ARG, "mlc_error_clear: null ctx");
+  if (ctx->err_dev == nullptr) return MLC_OK;
+  MLC_HIP(hipSetDevice(ctx->device));
+  MLC_HIP(hipDeviceSynchronize());
+  MLC_HIP(hipMemset(ctx->err_dev, 0, kErrorWordBytes));
+  for (size_t i = 0; i < kErrorWordBytes / sizeof(int32_t); ++i) ctx->err_host[i] = 0;
   return MLC_OK;
 }
 

@@ -1150,9 +1150,12 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             out.append("    for (int j = 0; j < V; ++j) {")
             out.append(f"      const float x = (float)({code});")
             out.append("      const float m_new = mlc::max_<float>(m_run, x);")
-            # m_new is the max of m_run and x: both exponents are at most 0
+            # m_new is the max of m_run and x: both exponents are at most 0.
+            # While every element this lane has seen is -inf, m_new is -inf
+            # too; subtracting 0 then keeps exp(-inf - -inf) from being NaN.
+            out.append("      const float m_sub = (m_new == (-__builtin_huge_valf())) ? 0.0f : m_new;")
             out.append("      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : mlc::exp_nonpos(m_run - m_new);")
-            out.append("      l_run = l_run * alpha + mlc::exp_nonpos(x - m_new);")
+            out.append("      l_run = l_run * alpha + mlc::exp_nonpos(x - m_sub);")
             out.append("      m_run = m_new;")
             out.append("    }")
         else:
@@ -1358,9 +1361,18 @@ def emit_kernel(k, cfg: Config) -> tuple[str, LaunchSpec] | None:
     raise TypeError(f"no HIP emitter for {type(k).__name__}")
 
 
-def generate_module(schedule: Schedule, cfg: Config) -> Module:
-    """Every generated kernel of ``schedule`` (and every extern op with a
-    native template) as one HIP translation unit."""
+def generate_module(schedule: Schedule, cfg: Config) -> str:
+    """The HIP source of every generated kernel of ``schedule`` (and of every
+    extern op with a native template), as one translation unit: the codegen
+    seam of ``mlc/codegen/triton_backend.py:261-287``. The launch table of
+    the same module is ``build_module(schedule, cfg).launches``."""
+    return build_module(schedule, cfg).source
+
+
+def build_module(schedule: Schedule, cfg: Config) -> Module:
+    """Source, launch table and per-symbol bodies of ``schedule``'s module.
+    Identical kernel bodies are emitted once, under a symbol named by the
+    body's hash."""
     functions: dict[str, str] = {}
     launches: dict[str, LaunchSpec] = {}
     for k in schedule.kernels:

@@ -184,13 +184,16 @@ class CompiledModel:
         if self._plan is None or buffers is not self._resident:
             for k in self.schedule.kernels:
                 self.run_one(k, buffers)
-            return
-        run = self._module.run_bound
-        for kind, payload in self._runs:
-            if kind == "extern":
-                run_bound_extern(payload)
-            elif kind == "kernel":
-                run(payload)
+        else:
+            run = self._module.run_bound
+            for kind, payload in self._runs:
+                if kind == "extern":
+                    run_bound_extern(payload)
+                elif kind == "kernel":
+                    run(payload)
+        fetch = getattr(self._module, "fetch_errors", None)
+        if fetch is not None:
+            fetch()
 
     def run_one(self, k, buffers: dict[str, torch.Tensor]) -> None:
         if isinstance(k, ExternKernel):
@@ -233,9 +236,34 @@ class CompiledModel:
         return outs[0] if len(outs) == 1 else tuple(outs)
 
     def __call__(self, *inputs: torch.Tensor):
+        self._raise_pending()
         if self.cfg.cuda_graphs and self.device.type == "cuda":
             return self._call_captured(inputs)
         return self.forward(*inputs)
+
+    # -- invalid inputs -------------------------------------------------------
+    def _raise_pending(self) -> None:
+        """Raise for an invalid input (an embedding id outside its table) that
+        an earlier, completed call met. The native gather cannot raise where
+        torch's ``aten.embedding`` would, so it flags the id in a device word
+        that every run copies back asynchronously; the flag is cleared before
+        raising, so the call after the exception runs normally."""
+        poll = getattr(self._module, "pending_error", None)
+        msg = poll() if poll is not None else None
+        if msg is not None:
+            self._module.clear_errors()
+            raise ExecutionError(msg)
+
+    def check_errors(self) -> None:
+        """Wait for every call so far to finish and raise
+        :class:`ExecutionError` if one of them met an invalid input."""
+        fetch = getattr(self._module, "fetch_errors", None)
+        if fetch is None:
+            return
+        fetch()
+        if self.device.type == "cuda":
+            torch.cuda.synchronize(self.device)
+        self._raise_pending()
 
     # -- graph replay -----------------------------------------------------------
     def _call_captured(self, inputs):
@@ -325,7 +353,8 @@ class CompiledModel:
 
     # -- introspection ------------------------------------------------------------
     def source(self) -> str:
-        return self._module.source()
+        """The generated module text (``mlc/runtime/executor.py:354-358``)."""
+        return self._module.source
 
     def source_path(self):
         return getattr(self._module, "path", None)

@@ -2,7 +2,8 @@
 
 The counterpart of the reference's ``TritonRuntime``
 (``mlc/runtime/triton_runtime.py:60-97``) behind the same seam: it is built
-from a schedule, exposes ``source``/``path``/``launch_table``, resolves a
+from a schedule, exposes ``source`` (the module text, a ``str``), ``path``
+(where that text was written) and ``launch_table``, resolves a
 kernel against the buffer table once (``bind``) and launches it
 (``launch``/``run_bound``) on torch's current stream. On top of that it owns
 the per-model native state the MI355X design adds:
@@ -14,7 +15,12 @@ the per-model native state the MI355X design adds:
   kernels run as one ``mlc_plan_run`` call (``compile_runs``);
 * hipGraph capture and replay of the whole schedule (``capture_begin``,
   ``capture_end``, ``replay``);
-* hipEvent timing of one bound kernel in place (``time_bound``).
+* hipEvent timing of one bound kernel in place (``time_bound``);
+* the invalid-input word: the native embedding gather flags an id outside
+  its table there (torch raises ``IndexError`` for one); every run enqueues
+  an asynchronous copy of the word to pinned host memory (``fetch_errors``,
+  captured into the graph too) and ``pending_error`` reads that copy without
+  waiting for the device.
 """
 
 from __future__ import annotations
@@ -25,7 +31,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ..codegen.hip_backend import LaunchSpec, generate_module
+from ..codegen.hip_backend import LaunchSpec, build_module
 from ..config import Config
 from ..kernels import ExternKernel, Kernel, Schedule
 from . import native
@@ -70,9 +76,11 @@ class HipRuntime:
         self.device = device
         self.index = device.index if device.index is not None else torch.cuda.current_device()
         self.lib = native.load_library()
-        self.module = generate_module(schedule, cfg)
+        self.module = build_module(schedule, cfg)
+        #: the generated HIP module text (``TritonRuntime.source``)
+        self.source: str = self.module.source
         self.launch_table: dict[str, LaunchSpec] = self.module.launches
-        self.path, self.code_object_path = native.compile_code_object(self.module.source)
+        self.path, self.code_object_path = native.compile_code_object(self.source)
         image = self.code_object_path.read_bytes()
 
         self._ctx = ctypes.c_void_p()
@@ -89,17 +97,15 @@ class HipRuntime:
             self.functions[symbol] = fn.value
         self._plans: list[ctypes.c_void_p] = []
         self._arena_tensor: torch.Tensor | None = None
-        #: set to non-zero by a kernel that met an invalid input (an embedding id
-        #: out of range); read back by ``check_errors``
-        self._error_word = torch.zeros(4, dtype=torch.int32, device=device)
+        #: device address of the context's invalid-input word, if a kernel
+        #: of this module can flag one (the native embedding gather)
+        self._error_word: int | None = None
+        if any(spec.meta.get("error_word") for spec in self.launch_table.values()):
+            word = ctypes.c_void_p()
+            native.check(self.lib.mlc_error_word(self._ctx, ctypes.byref(word)), "mlc_error_word")
+            self._error_word = word.value
 
     # -- the reference seam ---------------------------------------------------
-    @property
-    def source_text(self) -> str:
-        return self.module.source
-
-    def source(self) -> str:
-        return self.module.source
 
     def bind(self, k: Kernel, buffers: dict[str, torch.Tensor]) -> Bound:
         """Resolve a launch once: function handle, geometry and the packed
@@ -142,17 +148,55 @@ class HipRuntime:
                 raise native.NativeError(f"{k.name}: buffer {name} is not 16-byte aligned")
             ptrs.append(t.data_ptr())
         if spec.meta.get("error_word"):
-            ptrs.append(self._error_word.data_ptr())
+            ptrs.append(self._error_word)
         return Bound(k.name, self.functions[spec.symbol], spec.grid, spec.block, spec.lds_bytes,
                      struct.pack(f"<{len(ptrs)}Q", *ptrs))
 
+    # -- invalid inputs ------------------------------------------------------------
+    @property
+    def flags_errors(self) -> bool:
+        """Whether a kernel of this module can flag an invalid input."""
+        return self._error_word is not None
+
+    def fetch_errors(self, stream: int | None = None) -> None:
+        """Enqueue the copy of the invalid-input word to its pinned host
+        mirror on ``stream`` (torch's current stream by default). It is
+        issued after a run's kernels, so under capture it becomes the graph's
+        last node."""
+        if self._error_word is not None:
+            native.check(self.lib.mlc_error_fetch(self._ctx, _stream() if stream is None
+                                                  else stream), "mlc_error_fetch")
+
+    def pending_error(self) -> str | None:
+        """The message for an invalid input flagged by a completed run, read
+        from the host mirror without waiting for the device; ``None`` if no
+        completed run flagged one. Runs still in flight are seen by a later
+        call."""
+        if self._error_word is None:
+            return None
+        value = ctypes.c_int32()
+        native.check(self.lib.mlc_error_poll(self._ctx, ctypes.byref(value)), "mlc_error_poll")
+        if value.value == 0:
+            return None
+        return ("an embedding id was outside its table (torch raises IndexError for such an "
+                "id); the rows it addressed were written as zeros")
+
+    def clear_errors(self) -> None:
+        """Wait for the device, then zero the word and its mirror."""
+        if self._error_word is not None:
+            native.check(self.lib.mlc_error_clear(self._ctx), "mlc_error_clear")
+
     def check_errors(self) -> None:
-        """Raise if a kernel flagged an invalid input since the last check
-        (synchronizes with the device), then clear the flag."""
-        if int(self._error_word[0].item()) != 0:
-            self._error_word.zero_()
-            raise native.NativeError("an embedding id was outside the table; the affected rows "
-                                     "were written as zeros")
+        """Synchronize, fetch the word, and raise :class:`native.NativeError`
+        if any run so far flagged an invalid input (clearing the flag)."""
+        if self._error_word is None:
+            return
+        self.fetch_errors()
+        torch.cuda.synchronize(self.device)
+        msg = self.pending_error()
+        if msg is not None:
+            self.clear_errors()
+            raise native.NativeError(msg)
 
     def launch(self, k: Kernel, buffers: dict[str, torch.Tensor]) -> None:
         self.run_bound(self.bind(k, buffers))

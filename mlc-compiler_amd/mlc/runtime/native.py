@@ -105,6 +105,10 @@ SIGNATURES = {
     "mlc_graph_replay": ([_vp, _vp], _c_int),
     "mlc_graph_node_count": ([_vp, ctypes.POINTER(_c_size)], _c_int),
     "mlc_time_entry": ([_vp, _c_int, _c_int, _vp, ctypes.POINTER(ctypes.c_float)], _c_int),
+    "mlc_error_word": ([_vp, _pvp], _c_int),
+    "mlc_error_fetch": ([_vp, _vp], _c_int),
+    "mlc_error_poll": ([_vp, ctypes.POINTER(ctypes.c_int32)], _c_int),
+    "mlc_error_clear": ([_vp], _c_int),
     "mlc_device_synchronize": ([_vp], _c_int),
     "mlc_last_error": ([], ctypes.c_char_p),
 }

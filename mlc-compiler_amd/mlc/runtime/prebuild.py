@@ -19,7 +19,7 @@ import torch
 
 from ..api import build_pipeline
 from ..bench.workloads import WORKLOADS, make
-from ..codegen.hip_backend import generate_module
+from ..codegen.hip_backend import build_module
 from ..config import Config
 from ..ir.capture import capture
 from . import native
@@ -50,7 +50,7 @@ def prebuild(items=None, verbose: bool = True) -> None:
         model, args = make(key, "cpu")
         graph = capture(model, args)
         schedule = build_pipeline(graph, cfg)
-        module = generate_module(schedule, cfg)
+        module = build_module(schedule, cfg)
         _, obj = native.compile_code_object(module.source)
         if verbose:
             print(f"prebuild {key} max_row={cfg.max_persistent_row}: {len(module.functions)} "

@@ -31,10 +31,13 @@ Pinning (what fixes this oracle independently of itself):
   mistakes (a sign, exp2 for exp, a reduce identity) that must be caught
   (``tests/test_oracle.py``);
 * streamed evaluation agrees with persistent evaluation.
-One deliberate difference from the reference's torch backend: a reduction's
-row output is evaluated at one column, as the reference's Triton kernels
-compute it (``run_reduction``); the torch backend fails on a row output that
-reads a row-constant operand.
+Two deliberate differences from the reference's torch backend: a
+reduction's row output is evaluated at one column, as the reference's Triton
+kernels compute it (``run_reduction``; the torch backend fails on a row
+output that reads a row-constant operand), and the streamed online-softmax
+recurrence subtracts 0 instead of a running maximum that is still -inf (the
+torch backend returns NaN for a row whose first chunk is all -inf, where
+eager softmax is finite; pinned against eager in ``tests/test_oracle.py``).
 Transcendentals (exp/erf/tanh/...) are torch's CPU implementations:
 per-function parity against the reference's device libm is "parity
 unpinned"; only the end-to-end tolerances pin them, as in the reference.
@@ -206,7 +209,15 @@ def run_reduction(k: ReductionKernel, buffers: dict[str, torch.Tensor], chunk: i
                 if online is not None:
                     x = widen(online.value, loads, local, c1 - c0)
                     m_new = torch.maximum(m, x.amax(dim=1, keepdim=True))
-                    lsum = lsum * torch.exp(m - m_new) + torch.exp(x - m_new).sum(dim=1, keepdim=True)
+                    # a row whose elements so far are all -inf has m_new = -inf;
+                    # subtracting 0 there keeps exp(-inf - -inf) from being NaN
+                    # (the reference's torch backend subtracts m_new as is,
+                    # torch_backend.py:211-213, and returns NaN for such a
+                    # row where eager softmax is finite)
+                    inf = m_new == -float("inf")
+                    alpha = torch.where(m == -float("inf"), 0.0, torch.exp(m - m_new))
+                    m_sub = torch.where(inf, 0.0, m_new)
+                    lsum = lsum * alpha + torch.exp(x - m_sub).sum(dim=1, keepdim=True)
                     m = m_new
                 else:
                     for r in p.reduces:
@@ -305,6 +316,7 @@ class TorchReferenceRunner:
     executing the generated kernels."""
 
     name = "torch"
+    source = "# torch reference oracle: no generated source"
 
     def bind(self, k, buffers):
         return (k, buffers)
@@ -314,6 +326,3 @@ class TorchReferenceRunner:
 
     def launch(self, k, buffers) -> None:
         run_kernel(k, buffers)
-
-    def source(self) -> str:
-        return "# torch reference oracle: no generated source"

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from mlc.api import build_pipeline
-from mlc.codegen.hip_backend import (classify_access, float_literal, generate_module,
+from mlc.codegen.hip_backend import (build_module, classify_access, float_literal, generate_module,
                                      reduction_geometry)
 from mlc.codegen.index import build_index, flat_index
 from mlc.config import Config
@@ -108,7 +108,7 @@ def test_float_literals_are_exact_fp32():
 @pytest.mark.parametrize("name", [m[0] for m in all_models()])
 def test_launch_table_covers_every_generated_kernel(name, cfg):
     sched = _sched(name, cfg)
-    mod = generate_module(sched, cfg)
+    mod = build_module(sched, cfg)
     for k in sched.kernels:
         if isinstance(k, ExternKernel):
             continue
@@ -122,14 +122,25 @@ def test_launch_table_covers_every_generated_kernel(name, cfg):
 
 
 def test_generation_is_deterministic():
-    a = generate_module(_sched("block"), FULL).source
-    b = generate_module(_sched("block"), FULL).source
+    a = build_module(_sched("block"), FULL).source
+    b = build_module(_sched("block"), FULL).source
     assert a == b
+
+
+def test_generate_module_returns_the_source_text():
+    """The codegen seam returns the module text itself, as the reference's
+    ``generate_module(schedule, cfg) -> str`` does
+    (``mlc/codegen/triton_backend.py:261-287``); the launch table is
+    ``build_module``'s."""
+    sched = _sched("block")
+    src = generate_module(sched, FULL)
+    assert isinstance(src, str)
+    assert src == build_module(sched, FULL).source
 
 
 def test_layers_share_kernel_code():
     sched = build_pipeline(graph_of("C2"), Config())
-    mod = generate_module(sched, Config())
+    mod = build_module(sched, Config())
     generated = [k for k in sched.kernels if not isinstance(k, ExternKernel)]
     assert len(generated) == 100
     assert len(mod.functions) < 16, "each transformer layer should reuse the same functions"
@@ -137,7 +148,7 @@ def test_layers_share_kernel_code():
 
 def test_fp16_contiguous_operands_move_in_128bit_packs():
     sched = build_pipeline(graph_of("C4"), Config())
-    mod = generate_module(sched, Config())
+    mod = build_module(sched, Config())
     gelu = next(k for k in sched.kernels if isinstance(k, PointwiseKernel)
                 and any(n.op == "aten.erf.default" for n in k.nodes))
     spec = mod.launches[gelu.name]
@@ -150,7 +161,7 @@ def test_fp16_contiguous_operands_move_in_128bit_packs():
 
 def test_embedding_runs_as_a_native_template():
     sched = build_pipeline(graph_of("C2"), Config())
-    mod = generate_module(sched, Config())
+    mod = build_module(sched, Config())
     embs = [k for k in sched.kernels if isinstance(k, ExternKernel)
             and k.node.op == "aten.embedding.default"]
     assert len(embs) == 3
@@ -164,7 +175,7 @@ def test_embedding_runs_as_a_native_template():
 
 
 def test_no_packed_fp32_by_hand_and_no_scalar_stores():
-    src = generate_module(_sched("block"), FULL).source
+    src = build_module(_sched("block"), FULL).source
     text = src + native.TEMPLATES.joinpath("mlc_cdna4.h").read_text()
     assert not re.search(r"v_pk_(add|mul|fma)_f32", text)
     assert "-packed-fp32-ops" in native.HIP_FLAGS
@@ -175,7 +186,7 @@ def test_no_packed_fp32_by_hand_and_no_scalar_stores():
                                       ("masked", FULL), ("layernorm_scale", STREAMED)])
 def test_module_cross_compiles_for_gfx950(name, cfg, tmp_path, monkeypatch):
     monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
-    mod = generate_module(_sched(name, cfg), cfg)
+    mod = build_module(_sched(name, cfg), cfg)
     src, obj = native.compile_code_object(mod.source)
     assert obj.stat().st_size > 0 and src.read_text() == mod.source
     # cached: a second request does not recompile
@@ -200,7 +211,7 @@ def test_softmax_exp_has_no_overflow_path():
     import torch.nn as nn
 
     from mlc.api import build_pipeline
-    from mlc.codegen.hip_backend import generate_module
+    from mlc.codegen.hip_backend import build_module
     from mlc.config import Config
     from mlc.ir.capture import capture
 
@@ -210,7 +221,7 @@ def test_softmax_exp_has_no_overflow_path():
 
     x = torch.randn(8, 64)
     cfg = Config(cuda_graphs=False)
-    src = generate_module(build_pipeline(capture(Soft(), (x,)), cfg), cfg).source
+    src = build_module(build_pipeline(capture(Soft(), (x,)), cfg), cfg).source
     body = src[src.index('extern "C"'):]
     assert "mlc::exp_nonpos(" in body and "mlc::div_rcp_finite(" in body
     assert "mlc::exp_(" in body

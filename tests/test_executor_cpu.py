@@ -122,3 +122,95 @@ def test_externs_without_tensor_inputs_run_once_into_their_own_memory():
     assert arena is None or not (arena.data_ptr() <= t.data_ptr() < arena.data_ptr() + arena.numel())
     torch.testing.assert_close(got, Fill()(x))
     torch.testing.assert_close(compiled(x * 3.0), Fill()(x * 3.0))
+
+
+class _FlaggingRunner:
+    """The oracle runner plus a CPU stand-in for the native embedding gather:
+    an id outside the table yields a zero row and sets an error flag, which
+    ``pending_error`` reports, the way the HIP runtime reports its device
+    word's host mirror."""
+
+    name = "torch"
+    source = "# oracle"
+
+    def __init__(self):
+        from oracle import TorchReferenceRunner
+
+        self._inner = TorchReferenceRunner()
+        self.flag = 0
+        self.fetches = 0
+
+    def bind(self, k, buffers):
+        return self._inner.bind(k, buffers)
+
+    def launch(self, k, buffers):
+        self._inner.launch(k, buffers)
+
+    def bind_native_extern(self, k, buffers):
+        if k.node.op != "aten.embedding.default":
+            return None
+        return ("gather", k, buffers)
+
+    def run_bound(self, payload):
+        if payload[0] != "gather":
+            self._inner.run_bound(payload)
+            return
+        _, k, buffers = payload
+        weight, ids = k.node.args[0], k.node.args[1]
+        w = weight.layout.as_torch(buffers[weight.buffer.name])
+        i = ids.layout.as_torch(buffers[ids.buffer.name]).reshape(-1)
+        ok = (i >= 0) & (i < w.shape[0])
+        rows = torch.where(ok[:, None], w[i.clamp(0, w.shape[0] - 1)], torch.zeros_like(w[:1]))
+        out = k.node.outputs[0]
+        out.layout.as_torch(buffers[out.buffer.name]).copy_(rows.reshape(out.shape))
+        if not bool(ok.all()):
+            self.flag = 1
+
+    def fetch_errors(self):
+        self.fetches += 1
+
+    def pending_error(self):
+        return "an embedding id was outside its table" if self.flag else None
+
+    def clear_errors(self):
+        self.flag = 0
+
+
+class _Embed(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.emb = torch.nn.Embedding(10, 8)
+
+    def forward(self, ids):
+        return self.emb(ids) * 2.0
+
+
+def test_invalid_embedding_id_raises_on_the_next_call():
+    """The executor's side of the invalid-input word: a call whose embedding
+    ids leave the table returns (its rows are zeros), the next call raises
+    ``ExecutionError`` and clears the flag, and the call after that runs
+    normally; ``check_errors`` raises at once. Every run fetches the word."""
+    from mlc.api import build_pipeline
+    from mlc.ir.capture import capture
+    from mlc.runtime.executor import CompiledModel
+
+    torch.manual_seed(0)
+    model = _Embed()
+    ids = torch.tensor([[1, 2, 3, 4]])
+    graph = capture(model, (ids,))
+    runner = _FlaggingRunner()
+    compiled = CompiledModel(graph, build_pipeline(graph, FULL), FULL, torch.device("cpu"),
+                             runner=runner)
+    want = model(ids)
+    torch.testing.assert_close(compiled(ids), want)
+    bad = torch.tensor([[1, 12, 3, -1]])
+    out = compiled(bad)
+    assert torch.equal(out[0, 1], torch.zeros(8)) and torch.equal(out[0, 3], torch.zeros(8))
+    with pytest.raises(ExecutionError, match="outside its table"):
+        compiled(ids)
+    torch.testing.assert_close(compiled(ids), want)
+    compiled(bad)
+    with pytest.raises(ExecutionError, match="outside its table"):
+        compiled.check_errors()
+    compiled.check_errors()
+    assert runner.fetches >= 5

@@ -157,14 +157,14 @@ def test_empty_reductions_launch_nothing_or_one_idle_pack(tmp_path, monkeypatch)
     Zero columns: one pack per row whose lanes are all out of range, so a row
     reduces to the identity without a load (a zero-length pack array would
     not compile for the device)."""
-    from mlc.codegen.hip_backend import generate_module
+    from mlc.codegen.hip_backend import build_module
     from mlc.runtime import native
 
     monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
     for name, grid in (("empty_rows_sum", 0), ("empty_cols_sum", 1)):
         model, args = _case(name)
         sched = build_pipeline(capture(model, args), CFG)
-        mod = generate_module(sched, CFG)
+        mod = build_module(sched, CFG)
         spec = mod.launches[sched.kernels[0].name]
         assert spec.grid == grid
     assert spec.meta["packs"] == 1 and "valid[p] =" in mod.functions[spec.symbol]

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from mlc.api import build_pipeline
-from mlc.codegen.hip_backend import generate_module
+from mlc.codegen.hip_backend import build_module
 from mlc.config import Config
 from mlc.ir.capture import capture
 
@@ -54,7 +54,7 @@ def _module(name, device):
     x = torch.empty(shape, device=device)
     model = cls()
     sched = build_pipeline(capture(model, (x,)), Config())
-    return model, sched, generate_module(sched, Config())
+    return model, sched, build_module(sched, Config())
 
 
 @pytest.mark.parametrize("name", sorted(CASES))
@@ -70,7 +70,7 @@ def test_large_buffers_get_64_bit_offsets(name):
 def test_small_buffers_keep_32_bit_offsets():
     x = torch.empty(4, 1024, device="meta")
     sched = build_pipeline(capture(Softmax(), (x,)), Config())
-    mod = generate_module(sched, Config())
+    mod = build_module(sched, Config())
     body = mod.functions[mod.launches[sched.kernels[0].name].symbol]
     assert "uint32_t" in body and "uint64_t" not in body
 

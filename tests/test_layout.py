@@ -8,7 +8,7 @@ import torch
 
 from mlc.api import build_pipeline
 from mlc.bench.models import build
-from mlc.codegen.hip_backend import generate_module
+from mlc.codegen.hip_backend import build_module
 from mlc.codegen.index import flat_index
 from mlc.config import Config
 from mlc.ir.types import Layout
@@ -55,7 +55,7 @@ def test_bert_b32_copies_merge_into_bias_adds():
               if [n.op for n in k.nodes] == ["aten.add.Tensor", "aten.clone.default"]]
     assert len(merged) == 36
     assert not verify(list(sched.plan.live_ranges.values()), sched.plan.offsets)
-    mod = generate_module(sched, LAYOUT)
+    mod = build_module(sched, LAYOUT)
     kinds = [mod.launches[k.name].meta["kind"] for k in merged]
     assert kinds.count("transpose") == 12 and kinds.count("pointwise") == 24
     assert base.counts()["pointwise"] == 99

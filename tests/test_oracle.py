@@ -114,6 +114,38 @@ class _Var(nn.Module):
         return z.var(dim=-1, unbiased=False)
 
 
+class _MaskedSoftmax(nn.Module):
+    """A causal ``masked_fill(-inf)`` softmax over ``x`` plus a padding mask
+    that hides the first ``pad`` columns of row 0."""
+
+    def __init__(self, pad: int):
+        super().__init__()
+        self.pad = pad
+
+    def forward(self, x):
+        t = x.shape[-1]
+        causal = torch.ones(t, t, dtype=torch.bool, device=x.device).triu(1)[: x.shape[-2]]
+        hidden = causal.clone()
+        hidden[0, : self.pad] = True
+        hidden[0, -1] = False
+        return x.masked_fill(hidden, float("-inf")).softmax(dim=-1)
+
+
+@pytest.mark.parametrize("rows,cols,pad", [(96, 128, 100), (4, 2100, 1500)])
+def test_streamed_softmax_with_all_inf_prefix(rows, cols, pad):
+    """Streamed online softmax where a row's first columns (and, for the
+    wide rows, its whole first 1024-column chunk) are -inf: finite and equal
+    to eager softmax, as the persistent form is."""
+    torch.manual_seed(0)
+    x = torch.randn(rows, cols)
+    model = _MaskedSoftmax(pad)
+    want = model(x)
+    assert torch.isfinite(want).all()
+    for cfg in (FULL, STREAMED):
+        got = compile_reference(model, (x,), cfg)(x)
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6)
+
+
 def test_softmax_is_stable_on_large_logits():
     x = torch.randn(4, 64) * 100
     for cfg in (FULL, STREAMED):
