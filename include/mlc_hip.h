@@ -76,6 +76,21 @@ int mlc_slab_alloc(mlc_ctx* ctx, size_t bytes, void** dptr);
  * from_dlpack; its deleter releases one reference on the slab. */
 int mlc_slab_dlpack(mlc_ctx* ctx, void** managed_tensor);
 
+/* The arena for callers that cannot allocate (code under graph capture,
+ * serving loops, harnesses that forbid hipMalloc). It has no counterpart in
+ * the reference: a variant of mlc_slab_alloc that allocates nothing. The
+ * context's arena becomes the library's static device array of
+ * MLC_STATIC_SLAB_BYTES (one per GPU, 256-B aligned, held from the first
+ * context on that GPU until the process ends; its address is resolved once
+ * per device in mlc_ctx_create). Returns MLC_E_RANGE for `bytes` beyond the
+ * maximum and MLC_E_STATE if the context already holds an allocated slab.
+ * Calls no hipMalloc, hipFree or other allocating routine. Every context on
+ * one GPU that uses it shares the one array, which keeps the last run's
+ * contents (the planner writes every arena buffer before reading it, so
+ * nothing needs clearing): runs that overlap on one GPU race. */
+#define MLC_STATIC_SLAB_BYTES (64u << 20)
+int mlc_slab_static(mlc_ctx* ctx, size_t bytes, void** dptr);
+
 /* Launch one kernel; `kernarg` holds `size` bytes of packed arguments. */
 int mlc_launch(mlc_fn fn, uint32_t grid, uint32_t block, uint32_t lds_bytes,
                const void* kernarg, size_t size, void* stream);

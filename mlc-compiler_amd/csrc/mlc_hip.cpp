@@ -10,6 +10,7 @@
 #include <atomic>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -70,10 +71,16 @@ struct Slab {
   size_t bytes = 0;
   int device = 0;
   std::atomic<int> refs{1};
+  // the device's static arena (``scratch``): never freed, never deleted
+  bool is_static = false;
 };
 
 void slab_release(Slab* s) {
   if (s == nullptr) return;
+  if (s->is_static) {
+    s->refs.fetch_sub(1);
+    return;
+  }
   if (s->refs.fetch_sub(1) == 1) {
     if (s->ptr != nullptr) {
       int prev = 0;
@@ -116,6 +123,37 @@ int launch_raw(hipFunction_t fn, uint32_t grid, uint32_t block, uint32_t lds, co
   return MLC_OK;
 }
 
+// ---- the arena for callers that cannot allocate (mlc_slab_static)
+//
+// One array per GPU, held from the first context on that GPU until the
+// process ends. Its name is a host-side stand-in: the device address comes
+// from hipGetSymbolAddress, resolved once per device with that device
+// current (in mlc_ctx_create) and kept in g_static[device].
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[MLC_STATIC_SLAB_BYTES];
+
+struct StaticSlab {
+  std::once_flag once;
+  hipError_t status = hipSuccess;
+  Slab slab;
+};
+StaticSlab g_static[kMaxDevices];
+
+void resolve_static_slab(int device) {
+  StaticSlab& st = g_static[device];
+  std::call_once(st.once, [&st, device]() {
+    void* ptr = nullptr;
+    st.status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (st.status == hipSuccess) {
+      st.slab.ptr = ptr;
+      st.slab.bytes = MLC_STATIC_SLAB_BYTES;
+      st.slab.device = device;
+      st.slab.is_static = true;
+      st.slab.refs.store(0);
+    }
+  });
+}
+
 }  // namespace
 
 struct mlc_ctx {
@@ -152,6 +190,7 @@ int mlc_ctx_create(int device, mlc_ctx** out) {
   MLC_HIP(hipGetDeviceCount(&count));
   if (device < 0 || device >= count) return fail(MLC_E_RANGE, "mlc_ctx_create: no such device");
   MLC_HIP(hipSetDevice(device));
+  if (device < kMaxDevices) resolve_static_slab(device);
   mlc_ctx* c = new (std::nothrow) mlc_ctx;
   if (c == nullptr) return fail(MLC_E_STATE, "mlc_ctx_create: out of host memory");
   c->device = device;
@@ -214,6 +253,8 @@ int mlc_slab_alloc(mlc_ctx* ctx, size_t bytes, void** dptr) {
     *dptr = ctx->slab->ptr;
     return MLC_OK;
   }
+  if (ctx->slab != nullptr && ctx->slab->is_static)
+    return fail(MLC_E_STATE, "mlc_slab_alloc: the context's arena is the static one");
   if (ctx->slab != nullptr && ctx->slab->refs.load() > 1)
     return fail(MLC_E_STATE, "mlc_slab_alloc: cannot grow a slab that is still exported");
   MLC_HIP(hipSetDevice(ctx->device));
@@ -230,6 +271,31 @@ int mlc_slab_alloc(mlc_ctx* ctx, size_t bytes, void** dptr) {
   s->device = ctx->device;
   ctx->slab = s;
   *dptr = p;
+  return MLC_OK;
+}
+
+int mlc_slab_static(mlc_ctx* ctx, size_t bytes, void** dptr) {
+  if (ctx == nullptr || dptr == nullptr) return fail(MLC_E_ARG, "mlc_slab_static: bad argument");
+  if (bytes > MLC_STATIC_SLAB_BYTES)
+    return fail(MLC_E_RANGE, "mlc_slab_static: " + std::to_string(bytes) +
+                                 " bytes requested, the static arena holds " +
+                                 std::to_string(static_cast<size_t>(MLC_STATIC_SLAB_BYTES)));
+  if (ctx->device >= kMaxDevices)
+    return fail(MLC_E_RANGE, "mlc_slab_static: device index beyond the static arena table");
+  StaticSlab& st = g_static[ctx->device];
+  if (st.status != hipSuccess) return hip_fail(st.status, "mlc_slab_static: hipGetSymbolAddress");
+  if (st.slab.ptr == nullptr) return fail(MLC_E_STATE, "mlc_slab_static: static arena unresolved");
+  if (ctx->slab == &st.slab) {
+    *dptr = st.slab.ptr;
+    return MLC_OK;
+  }
+  if (ctx->slab != nullptr)
+    return fail(MLC_E_STATE,
+                "mlc_slab_static: the context already owns an allocated slab (freeing it "
+                "would call hipFree)");
+  st.slab.refs.fetch_add(1);
+  ctx->slab = &st.slab;
+  *dptr = st.slab.ptr;
   return MLC_OK;
 }
 

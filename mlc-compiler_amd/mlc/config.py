@@ -36,6 +36,12 @@ class Config:
     #: probabilities never stored). A schedule change, off by default.
     fused_attention: bool = False
 
+    #: bind the arena to the runtime library's static device array
+    #: (``mlc_slab_static``: no hipMalloc, at most 64 MiB, shared by every
+    #: model on the GPU that sets it, so their calls must not overlap)
+    #: instead of a slab of its own. Changes no schedule.
+    static_arena: bool = False
+
     # codegen
     pointwise_block: int = 1024
     #: longest row a persistent reduction holds; longer rows are streamed

@@ -97,6 +97,7 @@ class HipRuntime:
             self.functions[symbol] = fn.value
         self._plans: list[ctypes.c_void_p] = []
         self._arena_tensor: torch.Tensor | None = None
+        self._static_arena = bool(getattr(cfg, "static_arena", False))
         #: device address of the context's invalid-input word, if a kernel
         #: of this module can flag one (the native embedding gather)
         self._error_word: int | None = None
@@ -246,13 +247,20 @@ class HipRuntime:
 
     # -- arena -----------------------------------------------------------------
     def arena(self, nbytes: int) -> torch.Tensor:
-        """The arena: one ``hipMalloc`` slab of at least ``nbytes``, as a uint8
-        tensor that aliases the slab (DLPack, no copy)."""
+        """The arena: one ``hipMalloc`` slab of at least ``nbytes``, or with
+        ``Config(static_arena=True)`` the library's static device array
+        (``mlc_slab_static``, nothing allocated), as a uint8 tensor that
+        aliases it (DLPack, no copy)."""
         if self._arena_tensor is not None and self._arena_tensor.numel() >= nbytes:
             return self._arena_tensor
         self._arena_tensor = None
         ptr = ctypes.c_void_p()
-        native.check(self.lib.mlc_slab_alloc(self._ctx, nbytes, ctypes.byref(ptr)), "mlc_slab_alloc")
+        if self._static_arena:
+            native.check(self.lib.mlc_slab_static(self._ctx, nbytes, ctypes.byref(ptr)),
+                         "mlc_slab_static")
+        else:
+            native.check(self.lib.mlc_slab_alloc(self._ctx, nbytes, ctypes.byref(ptr)),
+                         "mlc_slab_alloc")
         managed = ctypes.c_void_p()
         native.check(self.lib.mlc_slab_dlpack(self._ctx, ctypes.byref(managed)), "mlc_slab_dlpack")
         capsule = _PyCapsule_New(managed, _CAPSULE_NAME, None)

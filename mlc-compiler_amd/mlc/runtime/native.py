@@ -43,6 +43,10 @@ HIP_FLAGS = [
 ]
 
 
+#: size of the library's static arena (``MLC_STATIC_SLAB_BYTES`` in the header)
+STATIC_SLAB_BYTES = 64 << 20
+
+
 class NativeError(RuntimeError):
     """A failure inside libmlc_hip.so or while building native code."""
 
@@ -94,6 +98,7 @@ SIGNATURES = {
     "mlc_module_unload": ([_vp], _c_int),
     "mlc_function": ([_vp, ctypes.c_char_p, _pvp], _c_int),
     "mlc_slab_alloc": ([_vp, _c_size, _pvp], _c_int),
+    "mlc_slab_static": ([_vp, _c_size, _pvp], _c_int),
     "mlc_slab_dlpack": ([_vp, _pvp], _c_int),
     "mlc_launch": ([_vp, _c_u32, _c_u32, _c_u32, _vp, _c_size, _vp], _c_int),
     "mlc_plan_create": ([_vp, _c_int, _pvp], _c_int),
