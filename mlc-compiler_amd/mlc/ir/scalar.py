@@ -1,19 +1,25 @@
-"""Scalar expression IR: the per-element body of a fused kernel.
+"""Per-element expressions: the body language of fused kernels.
 
-The HIP backend renders these expressions into device C++; the CPU oracle
-evaluates the same expressions with torch ops. Expressions are immutable and
-hashable so they double as keys for common-subexpression elimination.
+A fused kernel's arithmetic is a DAG of five node kinds -- ``Load`` (an
+input operand at the current point), ``Ref`` (a temporary bound earlier in
+the kernel), ``Const``, ``Call`` (one function of :data:`FUNCTIONS`) and
+``Cast``. The HIP emitter renders the DAG to device C++, the test oracle
+evaluates it with torch ops; both read the same nodes. Nodes are frozen
+dataclasses, so equal subexpressions hash equal and serve as CSE keys.
 
-Reference behaviour followed: ``mlc/ir/scalar.py:23-225`` (node kinds, the
-function table with its arities, and the exact identities folded at build
-time).
+Construction goes through :func:`call`, which checks arity and applies the
+rewrites that are exact for every float (``x*1``, ``x/1``, ``1*x``, ``x+0``,
+``x-0``, ``0+x``) and folds literal arithmetic, as the reference's builder
+does (``mlc/ir/scalar.py:130-191``): the kernels then never see the
+``mm * 1 + bias * 1`` that decomposing ``addmm`` produces.
 """
 
 from __future__ import annotations
 
 import math
+import operator
 from dataclasses import dataclass
-from typing import Any
+from typing import Any, Callable, Iterator
 
 import torch
 
@@ -24,15 +30,11 @@ class Expr:
 
 @dataclass(frozen=True)
 class Load(Expr):
-    """The kernel operand in input slot ``slot``, read at the current point."""
-
     slot: int
 
 
 @dataclass(frozen=True)
 class Ref(Expr):
-    """A temporary bound earlier in the same kernel (a body line or a reduce)."""
-
     name: str
 
 
@@ -54,117 +56,133 @@ class Cast(Expr):
     dtype: torch.dtype
 
 
-def cast(x: Expr, dtype: torch.dtype) -> Expr:
-    """Cast ``x``; a literal absorbs the dtype instead of getting a Cast node."""
-    if isinstance(x, Const):
-        return Const(x.value, dtype)
-    return Cast(x, dtype)
-
+# --------------------------------------------------------------------------
+# the function table
+# --------------------------------------------------------------------------
 
 @dataclass(frozen=True)
 class FnSpec:
     arity: int
+    #: the result is torch.bool whatever the operands are
     bool_result: bool = False
+    #: defined for floating-point operands only
     float_only: bool = False
 
 
-def _table() -> dict[str, FnSpec]:
-    t: dict[str, FnSpec] = {}
-    for n in ("neg", "abs", "floor"):
-        t[n] = FnSpec(1)
-    for n in ("reciprocal", "exp", "log", "sqrt", "rsqrt", "sin", "cos", "tanh",
-              "erf", "sigmoid"):
-        t[n] = FnSpec(1, float_only=True)
-    t["logical_not"] = FnSpec(1, bool_result=True)
-    for n in ("add", "sub", "mul", "div", "pow", "maximum", "minimum"):
-        t[n] = FnSpec(2)
-    for n in ("gt", "lt", "ge", "le", "eq", "ne", "logical_and", "logical_or"):
-        t[n] = FnSpec(2, bool_result=True)
-    t["where"] = FnSpec(3)
-    return t
+def _spec_table() -> dict[str, FnSpec]:
+    # name -> (arity, flags); "b" = bool result, "f" = float operands only
+    rows = """
+        neg 1 -     abs 1 -     floor 1 -    logical_not 1 b
+        reciprocal 1 f  exp 1 f  log 1 f  sqrt 1 f  rsqrt 1 f
+        sin 1 f  cos 1 f  tanh 1 f  erf 1 f  sigmoid 1 f
+        add 2 -  sub 2 -  mul 2 -  div 2 -  pow 2 -  maximum 2 -  minimum 2 -
+        gt 2 b  lt 2 b  ge 2 b  le 2 b  eq 2 b  ne 2 b  logical_and 2 b  logical_or 2 b
+        where 3 -
+    """.split()
+    return {name: FnSpec(int(arity), bool_result=flag == "b", float_only=flag == "f")
+            for name, arity, flag in zip(rows[0::3], rows[1::3], rows[2::3])}
 
 
-#: every scalar function a kernel body may use
-FUNCTIONS: dict[str, FnSpec] = _table()
+#: every function a kernel body may call, with its arity and result kind
+FUNCTIONS: dict[str, FnSpec] = _spec_table()
 
 
-def call(fn: str, *args: Expr) -> Expr:
-    spec = FUNCTIONS.get(fn)
-    if spec is None:
-        raise KeyError(f"unknown scalar function {fn!r}")
-    if len(args) != spec.arity:
-        raise ValueError(f"{fn} takes {spec.arity} args, got {len(args)}")
-    for a in args:
-        if not isinstance(a, Expr):
-            raise TypeError(f"{fn} arg is {type(a).__name__}, expected Expr")
-    folded = _fold(fn, args)
-    return folded if folded is not None else Call(fn, tuple(args))
+# --------------------------------------------------------------------------
+# construction
+# --------------------------------------------------------------------------
+
+def cast(x: Expr, dtype: torch.dtype) -> Expr:
+    """``x`` converted to ``dtype``; a literal takes the dtype itself."""
+    return Const(x.value, dtype) if isinstance(x, Const) else Cast(x, dtype)
 
 
-def _is_literal(e: Expr, v) -> bool:
-    return isinstance(e, Const) and not isinstance(e.value, bool) and e.value == v
+#: fn -> (identity on the left, identity on the right); None: no such side
+_IDENTITIES: dict[str, tuple[Any, Any]] = {
+    "mul": (1, 1), "div": (None, 1), "add": (0, 0), "sub": (None, 0),
+}
 
-
-def _fold(fn: str, args: tuple[Expr, ...]) -> Expr | None:
-    """Identities exact for every float including NaN/inf (x*1, x/1, 1*x,
-    x+0, x-0, 0+x) and folding of all-literal arithmetic."""
-    if fn in ("mul", "div") and _is_literal(args[1], 1):
-        return args[0]
-    if fn == "mul" and _is_literal(args[0], 1):
-        return args[1]
-    if fn in ("add", "sub") and _is_literal(args[1], 0):
-        return args[0]
-    if fn == "add" and _is_literal(args[0], 0):
-        return args[1]
-    if all(isinstance(a, Const) for a in args):
-        value = _fold_literals(fn, [a.value for a in args])
-        if value is not None:
-            return Const(value)
-    return None
-
-
-_LITERAL_OPS = {
-    "add": lambda a, b: a + b,
-    "sub": lambda a, b: a - b,
-    "mul": lambda a, b: a * b,
-    "div": lambda a, b: a / b,
-    "neg": lambda a: -a,
-    "sqrt": math.sqrt,
-    "exp": math.exp,
+#: literal arithmetic folded at build time (Python float semantics)
+_LITERAL: dict[str, Callable] = {
+    "add": operator.add, "sub": operator.sub, "mul": operator.mul,
+    "div": operator.truediv, "neg": operator.neg, "sqrt": math.sqrt, "exp": math.exp,
 }
 
 
-def _fold_literals(fn: str, values: list):
-    op = _LITERAL_OPS.get(fn)
-    if op is None:
-        return None
+def _literal_equals(e: Expr, v: Any) -> bool:
+    # a bool literal is a mask value, never an arithmetic identity
+    return isinstance(e, Const) and type(e.value) is not bool and e.value == v
+
+
+def _simplified(fn: str, args: tuple[Expr, ...]) -> Expr | None:
+    left, right = _IDENTITIES.get(fn, (None, None))
+    if right is not None and _literal_equals(args[1], right):
+        return args[0]
+    if left is not None and _literal_equals(args[0], left):
+        return args[1]
+    op = _LITERAL.get(fn)
+    if op is not None and all(isinstance(a, Const) for a in args):
+        try:
+            return Const(op(*(a.value for a in args)))
+        except (ZeroDivisionError, ValueError, OverflowError):
+            return None
+    return None
+
+
+def call(fn: str, *args: Expr) -> Expr:
+    """``fn(*args)``, checked against :data:`FUNCTIONS` and simplified."""
     try:
-        return op(*values)
-    except (ZeroDivisionError, ValueError, OverflowError):
-        return None
+        spec = FUNCTIONS[fn]
+    except KeyError:
+        raise KeyError(f"scalar function {fn!r} is not in the kernel function table") from None
+    if len(args) != spec.arity:
+        raise ValueError(f"scalar function {fn} expects {spec.arity} operand(s), got {len(args)}")
+    bad = [type(a).__name__ for a in args if not isinstance(a, Expr)]
+    if bad:
+        raise TypeError(f"scalar function {fn}: operand of type {bad[0]} is not an Expr")
+    return _simplified(fn, args) or Call(fn, tuple(args))
 
 
-def walk(e: Expr):
-    """Every subexpression of ``e``, children first."""
+# --------------------------------------------------------------------------
+# traversal
+# --------------------------------------------------------------------------
+
+def _children(e: Expr) -> tuple[Expr, ...]:
     if isinstance(e, Call):
-        for a in e.args:
-            yield from walk(a)
-    elif isinstance(e, Cast):
-        yield from walk(e.x)
-    yield e
+        return e.args
+    if isinstance(e, Cast):
+        return (e.x,)
+    return ()
+
+
+def walk(e: Expr) -> Iterator[Expr]:
+    """Every subexpression of ``e`` in post-order (operands left to right,
+    then the node), shared subtrees once per use."""
+    stack: list[tuple[Expr, bool]] = [(e, False)]
+    while stack:
+        node, expanded = stack.pop()
+        if expanded:
+            yield node
+            continue
+        stack.append((node, True))
+        stack.extend((c, False) for c in reversed(_children(node)))
 
 
 def loads(e: Expr) -> set[int]:
-    return {s.slot for s in walk(e) if isinstance(s, Load)}
+    """Input slots ``e`` reads."""
+    return {x.slot for x in walk(e) if isinstance(x, Load)}
 
 
 def refs(e: Expr) -> set[str]:
-    return {s.name for s in walk(e) if isinstance(s, Ref)}
+    """Temporaries ``e`` reads."""
+    return {x.name for x in walk(e) if isinstance(x, Ref)}
 
 
 def substitute(e: Expr, mapping: dict[Expr, Expr]) -> Expr:
-    if e in mapping:
-        return mapping[e]
+    """``e`` with every subexpression that is a key of ``mapping`` replaced
+    (outermost match wins; replacements are not rewritten again)."""
+    hit = mapping.get(e)
+    if hit is not None:
+        return hit
     if isinstance(e, Call):
         return Call(e.fn, tuple(substitute(a, mapping) for a in e.args))
     if isinstance(e, Cast):
@@ -173,5 +191,5 @@ def substitute(e: Expr, mapping: dict[Expr, Expr]) -> Expr:
 
 
 def size(e: Expr) -> int:
-    """Distinct nodes in the expression DAG."""
+    """Distinct nodes of the DAG rooted at ``e``."""
     return len(set(walk(e)))

@@ -1,12 +1,20 @@
-"""Storage and views.
+"""Storage and the views over it.
 
-A :class:`Buffer` is one contiguous allocation: the unit the planner places
-in the arena and the unit a kernel stores into. A :class:`Layout` is a
-``(shape, strides, offset)`` window onto a buffer. Every view op (permute,
-expand, slice, reshape that needs no copy) only builds a new Layout, so views
-never reach a kernel as work of their own.
+Two types carry every tensor in the IR:
 
-Reference behaviour followed: ``mlc/ir/types.py:38-263``.
+* :class:`Buffer` -- one dense allocation (name, shape, dtype, kind). It is
+  what the arena planner places and what a kernel stores into.
+* :class:`Layout` -- an affine window ``(shape, strides, offset)`` in elements
+  over some buffer. View ops only ever produce a new Layout, so a transpose,
+  a slice or a broadcast costs nothing and later shows up in a kernel's index
+  map instead of as a copy.
+
+The one non-trivial view is ``reshape``: it is free exactly when every new
+dimension falls inside one *chunk* of the old layout, a maximal group of
+adjacent dims that step through memory as one dense run. That is the rule
+``Tensor.view`` applies (reference counterpart: ``mlc/ir/types.py:148-218``);
+it is implemented here chunk by chunk (``_chunks`` then ``_fit``), and the
+resulting strides, size-1 dims included, are torch's.
 """
 
 from __future__ import annotations
@@ -22,149 +30,169 @@ Strides = tuple[int, ...]
 
 
 def contiguous_strides(shape: Sequence[int]) -> Strides:
-    """Row-major strides for ``shape``."""
-    out = []
-    step = 1
-    for d in reversed(tuple(shape)):
-        out.append(step)
-        step *= int(d)
-    return tuple(reversed(out))
+    """Row-major strides of ``shape`` (the last dim moves fastest)."""
+    dims = [int(d) for d in shape]
+    suffix = [math.prod(dims[i + 1:]) for i in range(len(dims))]
+    return tuple(suffix)
 
 
-def _numel(shape: Sequence[int]) -> int:
-    return math.prod(shape) if shape else 1
+def _chunks(shape: Shape, strides: Strides) -> list[tuple[int, int]]:
+    """The old layout cut into dense runs, innermost first, as
+    ``(elements, stride of the run's innermost dim)``. A dim continues the
+    run inside it when it is size 1 or steps exactly over that run."""
+    out: list[tuple[int, int]] = []
+    count, base = 1, strides[-1]
+    for d in range(len(shape) - 1, -1, -1):
+        count *= shape[d]
+        outer = d - 1
+        if outer >= 0 and (shape[outer] == 1 or strides[outer] == count * base):
+            continue
+        out.append((count, base))
+        if outer >= 0:
+            count, base = 1, strides[outer]
+    return out
+
+
+def _fit(chunks: list[tuple[int, int]], new_shape: Shape) -> Strides | None:
+    """Strides for ``new_shape`` such that every new dim lies in one chunk,
+    or None. New dims are handed out innermost first; a chunk takes dims
+    until it is covered, plus any size-1 dims that follow."""
+    strides = [0] * len(new_shape)
+    pos = len(new_shape) - 1
+    for count, base in chunks:
+        covered = 1
+        while pos >= 0 and (covered < count or new_shape[pos] == 1):
+            strides[pos] = covered * base
+            covered *= new_shape[pos]
+            pos -= 1
+        if covered != count:
+            return None
+    return tuple(strides) if pos < 0 else None
 
 
 @dataclass(frozen=True)
 class Layout:
+    """``element(i0, .., ik) = buffer[offset + sum(i_d * strides[d])]``."""
+
     shape: Shape
     strides: Strides
     offset: int = 0
 
     def __post_init__(self) -> None:
         if len(self.shape) != len(self.strides):
-            raise ValueError(f"rank mismatch: shape={self.shape} strides={self.strides}")
-        for d in self.shape:
-            if d < 0:
-                raise ValueError(f"negative dim in {self.shape}")
+            raise ValueError(f"layout has {len(self.shape)} sizes but {len(self.strides)} "
+                             f"strides ({self.shape} / {self.strides})")
+        if min(self.shape, default=0) < 0:
+            raise ValueError(f"layout size below zero: {self.shape}")
 
-    @staticmethod
-    def contiguous(shape: Sequence[int], offset: int = 0) -> "Layout":
-        shp = tuple(int(d) for d in shape)
-        return Layout(shp, contiguous_strides(shp), offset)
+    @classmethod
+    def contiguous(cls, shape: Sequence[int], offset: int = 0) -> "Layout":
+        dims = tuple(int(d) for d in shape)
+        return cls(dims, contiguous_strides(dims), offset)
 
-    # -- queries ------------------------------------------------------------
+    # -- properties -----------------------------------------------------------
     @property
     def rank(self) -> int:
         return len(self.shape)
 
     @property
     def numel(self) -> int:
-        return _numel(self.shape)
+        return math.prod(self.shape)
 
     def is_contiguous(self) -> bool:
         return self.offset == 0 and self.strides == contiguous_strides(self.shape)
 
     def is_dense_from_zero(self) -> bool:
+        """Covers exactly elements ``[0, numel)`` of its buffer in order."""
         return self.is_contiguous()
 
     def max_offset(self) -> int:
-        """One past the highest element offset reachable through this view."""
-        hi = self.offset
-        for n, s in zip(self.shape, self.strides):
-            if n > 0:
-                hi += (n - 1) * s
-        return hi + 1
+        """One past the furthest element this window reaches."""
+        reach = sum((d - 1) * s for d, s in zip(self.shape, self.strides) if d)
+        return self.offset + reach + 1
 
-    # -- view algebra -------------------------------------------------------
+    # -- views ----------------------------------------------------------------
+    def _with(self, dims: Iterable[tuple[int, int]], offset: int | None = None) -> "Layout":
+        pairs = list(dims)
+        return Layout(tuple(p[0] for p in pairs), tuple(p[1] for p in pairs),
+                      self.offset if offset is None else offset)
+
     def permute(self, dims: Sequence[int]) -> "Layout":
-        r = self.rank
-        order = [int(d) % r if r else 0 for d in dims]
-        if sorted(order) != list(range(r)):
-            raise ValueError(f"permute({list(dims)}) is not a permutation of rank {r}")
-        return Layout(tuple(self.shape[d] for d in order),
-                      tuple(self.strides[d] for d in order), self.offset)
+        order = [int(d) % max(self.rank, 1) for d in dims]
+        if len(order) != self.rank or set(order) != set(range(self.rank)):
+            raise ValueError(f"{list(dims)} does not reorder the {self.rank} dims of {self.shape}")
+        pairs = list(zip(self.shape, self.strides))
+        return self._with(pairs[d] for d in order)
 
     def expand(self, shape: Sequence[int]) -> "Layout":
-        """Broadcast to ``shape`` (``-1`` keeps a size); new dims get stride 0."""
+        """Broadcast to ``shape`` (-1 keeps a size): size-1 dims, and dims
+        added on the left, get stride 0."""
         want = [int(d) for d in shape]
-        if len(want) < self.rank:
-            raise ValueError(f"cannot expand rank {self.rank} to {len(want)} dims")
-        lead = len(want) - self.rank
-        have_shape = (1,) * lead + self.shape
-        have_strides = (0,) * lead + self.strides
-        shp: list[int] = []
-        std: list[int] = []
-        for i, w in enumerate(want):
-            h = have_shape[i]
-            if w == -1:
-                w = h
-            if w == h:
-                shp.append(w)
-                std.append(have_strides[i])
-            elif h == 1:
-                shp.append(w)
-                std.append(0)
+        extra = len(want) - self.rank
+        if extra < 0:
+            raise ValueError(f"expand to {want} has fewer dims than {self.shape}")
+        have = [(1, 0)] * extra + list(zip(self.shape, self.strides))
+        out = []
+        for i, ((size, stride), w) in enumerate(zip(have, want)):
+            w = size if w == -1 else w
+            if w == size:
+                out.append((size, stride))
+            elif size == 1:
+                out.append((w, 0))
             else:
-                raise ValueError(f"cannot expand dim {i} from {h} to {w}")
-        return Layout(tuple(shp), tuple(std), self.offset)
+                raise ValueError(f"expand {self.shape} -> {tuple(want)}: dim {i} has size "
+                                 f"{size}, not 1, and cannot become {w}")
+        return self._with(out)
 
     def unsqueeze(self, dim: int) -> "Layout":
-        if dim < 0:
-            dim += self.rank + 1
-        s = self.strides[dim] * self.shape[dim] if dim < self.rank else 1
-        return Layout(self.shape[:dim] + (1,) + self.shape[dim:],
-                      self.strides[:dim] + (s,) + self.strides[dim:], self.offset)
+        at = dim + self.rank + 1 if dim < 0 else dim
+        pairs = list(zip(self.shape, self.strides))
+        stride = pairs[at][0] * pairs[at][1] if at < self.rank else 1
+        pairs.insert(at, (1, stride))
+        return self._with(pairs)
 
     def squeeze(self, dims: Iterable[int] | None = None) -> "Layout":
         if dims is None:
-            keep = [i for i, n in enumerate(self.shape) if n != 1]
+            gone = {i for i, d in enumerate(self.shape) if d == 1}
         else:
-            gone = {int(d) % self.rank for d in dims}
-            keep = [i for i in range(self.rank)
-                    if not (i in gone and self.shape[i] == 1)]
-        return Layout(tuple(self.shape[i] for i in keep),
-                      tuple(self.strides[i] for i in keep), self.offset)
+            gone = {d % self.rank for d in dims if self.shape[d % self.rank] == 1}
+        return self._with(p for i, p in enumerate(zip(self.shape, self.strides))
+                          if i not in gone)
 
     def slice(self, dim: int, start: int, end: int, step: int = 1) -> "Layout":
-        dim %= self.rank
-        n = self.shape[dim]
-        lo = start + n if start < 0 else start
-        lo = min(max(lo, 0), n)
-        hi = end + n if end < 0 else end
-        hi = min(max(hi, lo), n)
-        length = (hi - lo + step - 1) // step
-        shp = list(self.shape)
-        std = list(self.strides)
-        shp[dim] = length
-        std[dim] = self.strides[dim] * step
-        return Layout(tuple(shp), tuple(std), self.offset + lo * self.strides[dim])
+        d = dim % self.rank
+        n = self.shape[d]
+
+        def clamp(v: int, lo: int) -> int:
+            return min(n, max(lo, v + n if v < 0 else v))
+
+        lo = clamp(start, 0)
+        hi = clamp(end, lo)
+        pairs = list(zip(self.shape, self.strides))
+        stride = pairs[d][1]
+        pairs[d] = (-(-(hi - lo) // step), stride * step)
+        return self._with(pairs, self.offset + lo * stride)
 
     def reshape(self, shape: Sequence[int]) -> "Layout | None":
-        """The same storage seen with ``shape``, or None when that needs a copy.
-
-        A reshape is free when it only splits or joins dimensions inside runs
-        that are contiguous in the existing layout (torch's ``view`` rule), so a
-        strided slice can still have its last dimension split into heads.
-        """
-        shp = tuple(int(d) for d in shape)
-        if _numel(shp) != self.numel:
-            raise ValueError(f"reshape {self.shape} -> {shp} changes element count")
+        """The same elements under ``shape`` without copying, or None when
+        some new dim would straddle two dense runs of this layout."""
+        dims = tuple(int(d) for d in shape)
+        if math.prod(dims) != self.numel:
+            raise ValueError(f"reshape {self.shape} -> {dims}: {self.numel} elements vs "
+                             f"{math.prod(dims)}")
         if self.numel == 0:
-            return Layout(shp, contiguous_strides(shp), self.offset)
-        strides = view_strides(self.shape, self.strides, shp)
-        if strides is None:
-            return None
-        return Layout(shp, strides, self.offset)
+            return Layout(dims, contiguous_strides(dims), self.offset)
+        if not self.shape:
+            return Layout(dims, (), self.offset) if not dims else None
+        strides = _fit(_chunks(self.shape, self.strides), dims)
+        return None if strides is None else Layout(dims, strides, self.offset)
 
     def as_torch(self, storage: torch.Tensor) -> torch.Tensor:
-        """This view over a flat 1-D ``storage`` tensor.
-
-        ``as_strided`` offsets are relative to the underlying storage, so the
-        flat tensor's own storage offset (non-zero for an arena slice) is added.
-        """
+        """This window over a flat 1-D ``storage`` tensor. ``as_strided``
+        counts its offset from the start of the *storage*, so a storage that
+        is itself a slice (an arena sub-range) adds its own offset."""
         return storage.as_strided(self.shape, self.strides,
-                                  self.offset + storage.storage_offset())
+                                  storage.storage_offset() + self.offset)
 
     def __repr__(self) -> str:  # pragma: no cover - debug aid
         if self.is_contiguous():
@@ -172,56 +200,23 @@ class Layout:
         return f"Layout{self.shape} strides={self.strides} off={self.offset}"
 
 
-def view_strides(old_shape: Shape, old_strides: Strides, new_shape: Shape) -> Strides | None:
-    """Strides that view ``old`` storage as ``new_shape``, or None.
-
-    Torch's stride computation for ``Tensor.view``: scan the old dims from the
-    innermost outwards, close a chunk wherever the next-outer dim is not laid
-    out directly after the current run, and require each chunk to be covered
-    exactly by a run of new dims.
-    """
-    out = [0] * len(new_shape)
-    vd = len(new_shape) - 1
-    unit = old_strides[-1] if old_shape else 1
-    chunk_elems = 1
-    covered = 1
-    for td in range(len(old_shape) - 1, -1, -1):
-        chunk_elems *= old_shape[td]
-        boundary = td == 0 or (old_shape[td - 1] != 1
-                               and old_strides[td - 1] != chunk_elems * unit)
-        if not boundary:
-            continue
-        while vd >= 0 and (covered < chunk_elems or new_shape[vd] == 1):
-            out[vd] = covered * unit
-            covered *= new_shape[vd]
-            vd -= 1
-        if covered != chunk_elems:
-            return None
-        if td > 0:
-            unit = old_strides[td - 1]
-            chunk_elems = 1
-            covered = 1
-    return tuple(out) if vd == -1 else None
-
-
 # --------------------------------------------------------------------------
-# Buffers
+# buffers
 # --------------------------------------------------------------------------
 
-#: buffer kinds the planner may place in the arena
-PLANNABLE = ("intermediate",)
-
+#: what a buffer holds; only intermediates are placed in the arena
 BUFFER_KINDS = ("input", "param", "intermediate", "output", "constant")
+PLANNABLE = ("intermediate",)
 
 _ITEMSIZE: dict[torch.dtype, int] = {}
 
 
 def itemsize_of(dtype: torch.dtype) -> int:
-    n = _ITEMSIZE.get(dtype)
-    if n is None:
-        n = torch.empty((), dtype=dtype).element_size()
-        _ITEMSIZE[dtype] = n
-    return n
+    """Bytes per element of ``dtype``."""
+    size = _ITEMSIZE.get(dtype)
+    if size is None:
+        size = _ITEMSIZE[dtype] = torch.empty((), dtype=dtype).element_size()
+    return size
 
 
 @dataclass(eq=False)
@@ -230,17 +225,18 @@ class Buffer:
     shape: Shape
     dtype: torch.dtype
     kind: str = "intermediate"
-    #: byte offset in the arena, set by the memory planner
+    #: byte offset in the arena, written by the planner (None: not placed)
     arena_offset: int | None = field(default=None, compare=False)
 
     def __post_init__(self) -> None:
-        self.shape = tuple(int(d) for d in self.shape)
         if self.kind not in BUFFER_KINDS:
-            raise ValueError(f"bad buffer kind {self.kind!r}")
+            raise ValueError(f"buffer {self.name}: kind {self.kind!r} is not one of "
+                             f"{BUFFER_KINDS}")
+        self.shape = tuple(int(d) for d in self.shape)
 
     @property
     def numel(self) -> int:
-        return _numel(self.shape)
+        return math.prod(self.shape)
 
     @property
     def itemsize(self) -> int:

@@ -1,16 +1,33 @@
-"""Kernel IR: the contract between the fusion passes and the backends.
+"""Kernel IR: what lowering hands to the HIP backend (and to the test oracle).
 
-A :class:`Schedule` is an ordered list of kernels. Each names the values it
-reads and writes (so the planner can compute live ranges) and carries, per
-operand, the index map it is read or written at. The HIP backend consumes
-exactly this; the CPU oracle executes the same objects.
+A :class:`Schedule` is the program: kernels in execution order. Every kernel
+exposes the same two questions the memory planner asks -- which values it
+reads (``reads``) and writes (``writes``) -- and, for the generated kinds, how
+it addresses each operand (a :class:`KernelArg`: value + :class:`IndexMap`
+over the kernel's iteration variables; pointers are buffer bases, view
+offsets live in the map's ``base``).
 
-Reference behaviour followed: ``mlc/kernels.py:23-232``.
+Kinds:
+
+* :class:`PointwiseKernel` -- one flat space ``idx``; ``body`` is a list of
+  ``(temp, Expr)`` lines, ``out_expr`` names what each output stores.
+* :class:`ReductionKernel` -- rows x columns; ``steps`` interleaves
+  ``Bind`` (per-element or per-row values) and ``Reduce`` (a cross-column
+  reduction) in evaluation order, so softmax is bind, reduce(max), bind,
+  bind, reduce(sum), bind over one load of the row. ``row_outputs`` are
+  stored once per row; ``two_pass`` marks rows streamed in chunks.
+* :class:`AttentionKernel` -- bmm, the reduction over its scores and the
+  bmm that consumes the probabilities, as one kernel (a schedule variant).
+* :class:`ExternKernel` -- a library call (GEMMs, opaque ops).
+
+Field names and the kinds' ``summary`` lines are the reference's kernel-IR
+contract (``mlc/kernels.py:23-232``); the golden schedules record them.
 """
 
 from __future__ import annotations
 
 import math
+from collections import Counter
 from dataclasses import dataclass, field
 
 import torch
@@ -22,47 +39,39 @@ from .ir.scalar import Expr
 
 @dataclass
 class KernelArg:
-    """One operand and the index map it is accessed by. Kernels receive the
-    buffer's base pointer; view offsets live in ``index.base``."""
-
     value: Value
     index: IndexMap
 
-    @property
-    def name(self) -> str:
-        return self.value.name
+    name = property(lambda self: self.value.name)
+    buffer = property(lambda self: self.value.buffer)
+    dtype = property(lambda self: self.value.dtype)
 
-    @property
-    def buffer(self):
-        return self.value.buffer
 
-    @property
-    def dtype(self) -> torch.dtype:
-        return self.value.dtype
+def _op_names(nodes: list[Node]) -> str:
+    """``aten.add.Tensor`` -> ``add``, comma separated."""
+    return ", ".join(n.op.rsplit(".", 2)[-2] for n in nodes)
 
 
 @dataclass
 class Kernel:
     name: str
 
+    # generated kernels keep KernelArg operands; ExternKernel overrides both
     def reads(self) -> list[Value]:
-        raise NotImplementedError
+        return [a.value for a in self.inputs]
 
     def writes(self) -> list[Value]:
-        raise NotImplementedError
+        return [a.value for a in self.outputs]
 
     def summary(self) -> str:
         return self.name
 
-
-def _op_names(nodes) -> str:
-    return ", ".join(n.op.split(".")[-2] for n in nodes)
+    def _arity(self) -> str:
+        return f"{len(self.inputs)}in {len(self.outputs)}out"
 
 
 @dataclass
 class PointwiseKernel(Kernel):
-    """``out_j[map_j(idx)] = body(in_k[map_k(idx)])`` for idx over ``space``."""
-
     space: tuple[int, ...]
     inputs: list[KernelArg]
     outputs: list[KernelArg]
@@ -72,22 +81,16 @@ class PointwiseKernel(Kernel):
 
     @property
     def numel(self) -> int:
-        return math.prod(self.space) if self.space else 1
-
-    def reads(self) -> list[Value]:
-        return [a.value for a in self.inputs]
-
-    def writes(self) -> list[Value]:
-        return [a.value for a in self.outputs]
+        return math.prod(self.space)
 
     def summary(self) -> str:
-        return (f"{self.name}: pointwise{list(self.space)} "
-                f"{len(self.inputs)}in {len(self.outputs)}out [{_op_names(self.nodes)}]")
+        return f"{self.name}: pointwise{list(self.space)} {self._arity()} [{_op_names(self.nodes)}]"
 
 
 @dataclass
 class Bind:
-    """A pointwise value computed inside a reduction kernel."""
+    """A value computed in the kernel (per element, or per row when it reads
+    only row values)."""
 
     name: str
     expr: Expr
@@ -95,10 +98,10 @@ class Bind:
 
 @dataclass
 class Reduce:
-    """A reduction over the column axis of the kernel's frame."""
+    """``kind`` (sum/max/min/prod) of ``expr`` across the row's columns."""
 
     name: str
-    kind: str  # "sum" | "max" | "min" | "prod"
+    kind: str
     expr: Expr
 
 
@@ -107,9 +110,6 @@ Step = Bind | Reduce
 
 @dataclass
 class ReductionKernel(Kernel):
-    """One row per program; ``steps`` interleave binds and reduces in order
-    (softmax is bind, max, bind, bind, sum, bind)."""
-
     row_space: tuple[int, ...]
     reduce_space: tuple[int, ...]
     inputs: list[KernelArg]
@@ -118,47 +118,32 @@ class ReductionKernel(Kernel):
     out_expr: dict[str, Expr]
     row_outputs: set[str] = field(default_factory=set)
     nodes: list[Node] = field(default_factory=list)
-    #: the row is longer than the persistent limit and is streamed
     two_pass: bool = False
 
-    @property
-    def reduce_numel(self) -> int:
-        return math.prod(self.reduce_space) if self.reduce_space else 1
-
-    @property
-    def n_rows(self) -> int:
-        return math.prod(self.row_space) if self.row_space else 1
+    n_rows = property(lambda self: math.prod(self.row_space))
+    reduce_numel = property(lambda self: math.prod(self.reduce_space))
 
     @property
     def reduces(self) -> list[Reduce]:
-        return [s for s in self.steps if isinstance(s, Reduce)]
-
-    def reads(self) -> list[Value]:
-        return [a.value for a in self.inputs]
-
-    def writes(self) -> list[Value]:
-        return [a.value for a in self.outputs]
+        return [s for s in self.steps if type(s) is Reduce]
 
     def summary(self) -> str:
         kinds = "+".join(r.kind for r in self.reduces) or "none"
-        mode = "streamed" if self.two_pass else "persistent"
-        return (f"{self.name}: reduction {self.n_rows}x{self.reduce_numel} {kinds} ({mode}) "
-                f"{len(self.inputs)}in {len(self.outputs)}out [{_op_names(self.nodes)}]")
+        how = "streamed" if self.two_pass else "persistent"
+        return (f"{self.name}: reduction {self.n_rows}x{self.reduce_numel} {kinds} ({how}) "
+                f"{self._arity()} [{_op_names(self.nodes)}]")
 
 
 @dataclass
 class AttentionKernel(Kernel):
-    """``out = steps(q @ kt) @ v`` per batch-head: a batched GEMM, the row
-    reduction that follows it and the batched GEMM that consumes that, as one
-    kernel (a schedule variant; the reference schedule keeps three). The
-    score and probability tensors are never stored, but their storage
-    roundings are kept: scores are rounded to ``score_dtype`` before the
-    reduction's steps and probabilities to ``prob_dtype`` before the second
-    GEMM, as the unfused schedule does.
+    """``out = steps(q @ kt) @ v`` per batch-head, scores and probabilities
+    kept in registers; their storage roundings are applied as the unfused
+    schedule stores them (scores to ``score_dtype`` before the reduction's
+    steps, probabilities to ``prob_dtype`` before the second product).
 
-    ``inputs`` are q, kt, v, then the reduction's other inputs (index maps
-    over its ``row``/``col`` frame); ``softmax`` is the original reduction
-    kernel, whose slot ``score_slot`` read the scores."""
+    ``inputs`` are q, kt, v, then the reduction's other operands (maps over
+    its row/col frame); ``softmax`` is the reduction kernel it absorbed, whose
+    slot ``score_slot`` read the scores."""
 
     q: Value
     kt: Value
@@ -172,12 +157,6 @@ class AttentionKernel(Kernel):
     outputs: list[KernelArg]
     nodes: list[Node] = field(default_factory=list)
 
-    def reads(self) -> list[Value]:
-        return [a.value for a in self.inputs]
-
-    def writes(self) -> list[Value]:
-        return [a.value for a in self.outputs]
-
     def summary(self) -> str:
         bh, t, d = self.q.shape
         return (f"{self.name}: attention {bh}x[{t}x{d}]x[{self.kt.shape[2]}] "
@@ -186,8 +165,6 @@ class AttentionKernel(Kernel):
 
 @dataclass
 class ExternKernel(Kernel):
-    """A library call (matmul, embedding, anything opaque)."""
-
     node: Node
     inputs: list[Value]
     outputs: list[Value]
@@ -199,14 +176,15 @@ class ExternKernel(Kernel):
         return list(self.outputs)
 
     def summary(self) -> str:
-        shapes = "x".join(str(list(v.shape)) for v in self.inputs)
-        return f"{self.name}: extern {self.node.op} {shapes}"
+        operands = "x".join(str(list(v.shape)) for v in self.inputs)
+        return f"{self.name}: extern {self.node.op} {operands}"
 
 
 @dataclass
 class Schedule:
     graph: object
     kernels: list[Kernel] = field(default_factory=list)
+    #: set by the planner
     arena_bytes: int = 0
     plan: object | None = None
 
@@ -217,18 +195,15 @@ class Schedule:
         return len(self.kernels)
 
     def counts(self) -> dict[str, int]:
-        out: dict[str, int] = {}
-        for k in self.kernels:
-            key = type(k).__name__.replace("Kernel", "").lower()
-            out[key] = out.get(key, 0) + 1
-        return out
+        """Kernels per kind: ``{"pointwise": .., "reduction": .., ...}``."""
+        return dict(Counter(type(k).__name__.removesuffix("Kernel").lower() for k in self.kernels))
 
     def format(self) -> str:
-        lines = [f"schedule({len(self.kernels)} kernels, {self.counts()})"]
-        lines += ["  " + k.summary() for k in self.kernels]
+        lines = [f"schedule({len(self)} kernels, {self.counts()})"]
+        lines += [f"  {k.summary()}" for k in self.kernels]
         if self.plan is not None:
-            lines.append("  " + self.plan.summary())
+            lines.append(f"  {self.plan.summary()}")
         return "\n".join(lines)
 
-    def __repr__(self) -> str:  # pragma: no cover
+    def __repr__(self) -> str:  # pragma: no cover - debug aid
         return self.format()

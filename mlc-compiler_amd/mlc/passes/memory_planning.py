@@ -1,39 +1,50 @@
-"""Memory planning: pack every intermediate buffer into one arena.
+"""The arena: every intermediate buffer at a fixed byte offset of one slab.
 
-Live ranges are kernel-index intervals per buffer (first write to last read;
-graph outputs live past the end). Packing is greedy: largest first (ties by
-first write, then name), each at the lowest 256-byte-aligned offset clear of
-every already-placed buffer whose range overlaps. The arena is then one
-``hipMalloc`` slab on the device, and these offsets are the byte offsets of
-each buffer inside it.
+Shapes are static and each intermediate buffer is written by one kernel and
+read by known later ones, so its lifetime is an interval of kernel indices.
+Buffers whose intervals are disjoint may share bytes. On the GPU the arena is
+one ``hipMalloc`` slab, and because every offset is fixed at compile time
+every kernel argument is the same pointer on every call -- what lets the whole
+schedule be captured once as a hipGraph and replayed.
 
-Reference behaviour followed: ``mlc/passes/memory_planning.py:35-240``. The
-packing order and the gap search are the reference's, so offsets and the
-arena size are bit-identical for the same schedule.
+Placement contract (kept bit-exact with the reference planner,
+``mlc/passes/memory_planning.py:35-240``, so offsets match its golden
+fixtures): buffers are taken largest first, ties by first-write index, then
+name; each goes to the lowest offset whose bytes no time-overlapping buffer
+already placed occupies; offsets and buffer sizes are multiples of 256 bytes.
+
+Besides placement the planner reports the lower bound no placement can beat
+(the most bytes live at one kernel) and checks its own result: any two
+buffers live at the same time must not share a byte.
 """
 
 from __future__ import annotations
 
+from collections import defaultdict
 from dataclasses import dataclass, field
+from itertools import accumulate
 
 from ..config import Config
 from ..ir.graph import Graph
 from ..ir.types import Buffer
 from ..kernels import Schedule
 
-#: byte alignment of every arena offset
+#: byte alignment of every arena offset (16-byte packs, library GEMM operands)
 ALIGNMENT = 256
 
 
-def _align(n: int, to: int = ALIGNMENT) -> int:
-    return -(-n // to) * to
+def _round_up(n: int) -> int:
+    return -(-n // ALIGNMENT) * ALIGNMENT
 
 
 @dataclass
 class LiveRange:
     buffer: Buffer
+    #: index of the kernel that first writes the buffer
     start: int
+    #: index of the last kernel touching it (len(schedule) for a graph output)
     end: int
+    #: bytes reserved (the buffer's size rounded up to ALIGNMENT)
     size: int
 
     def overlaps(self, other: "LiveRange") -> bool:
@@ -42,132 +53,147 @@ class LiveRange:
 
 @dataclass
 class AllocationPlan:
-    mode: str  # "arena" | "eager"
+    #: "arena" (placed in one slab) or "eager" (allocated around each kernel)
+    mode: str
     arena_bytes: int = 0
     offsets: dict[str, int] = field(default_factory=dict)
-    #: eager mode: kernel index -> buffers allocated just before it
+    #: eager mode: kernel index -> buffers to allocate before it runs
     alloc_at: dict[int, list[Buffer]] = field(default_factory=dict)
-    #: eager mode: kernel index -> buffer names released just after it
+    #: eager mode: kernel index -> buffer names to drop after it runs
     free_at: dict[int, list[str]] = field(default_factory=dict)
     live_ranges: dict[str, LiveRange] = field(default_factory=dict)
-    #: most bytes live at once: a lower bound for any arena
+    #: most bytes live at any one kernel: the bound no placement can beat
     peak_bytes: int = 0
-    #: sum of all plannable buffers
+    #: bytes if every buffer had memory of its own
     total_bytes: int = 0
 
     @property
     def efficiency(self) -> float:
+        """Arena size over the lower bound (1.0 is optimal)."""
         return self.arena_bytes / self.peak_bytes if self.peak_bytes else 1.0
 
     def summary(self) -> str:
-        if self.mode != "arena":
-            return (f"memory: unplanned, peak {self.peak_bytes / 1024:.1f} KiB "
-                    f"of {self.total_bytes / 1024:.1f} KiB total")
-        return (f"memory: arena {self.arena_bytes / 1024:.1f} KiB, "
-                f"lower bound {self.peak_bytes / 1024:.1f} KiB ({self.efficiency:.2f}x), "
-                f"unplanned would be {self.total_bytes / 1024:.1f} KiB")
+        kib = lambda n: f"{n / 1024:.1f} KiB"  # noqa: E731
+        if self.mode == "arena":
+            return (f"memory: arena {kib(self.arena_bytes)}, lower bound {kib(self.peak_bytes)} "
+                    f"({self.efficiency:.2f}x), unplanned would be {kib(self.total_bytes)}")
+        return f"memory: unplanned, peak {kib(self.peak_bytes)} of {kib(self.total_bytes)} total"
 
+
+# --------------------------------------------------------------------------
+# lifetimes
+# --------------------------------------------------------------------------
 
 def compute_live_ranges(graph: Graph, schedule: Schedule) -> list[LiveRange]:
-    """Per-buffer [first write, last read] over kernel indices."""
-    first_write: dict[str, int] = {}
-    last_use: dict[str, int] = {}
+    """Lifetimes of the plannable buffers, per *buffer* (a view keeps its
+    whole buffer alive), in order of first appearance in the schedule."""
+    first: dict[str, int] = {}
+    last: dict[str, int] = {}
     by_name: dict[str, Buffer] = {}
+
+    def touch(buf: Buffer, i: int, writes: bool) -> None:
+        by_name.setdefault(buf.name, buf)
+        if writes:
+            first.setdefault(buf.name, i)
+        last[buf.name] = max(last.get(buf.name, i), i)
+
     for i, k in enumerate(schedule.kernels):
         for v in k.writes():
-            nm = v.buffer.name
-            by_name.setdefault(nm, v.buffer)
-            first_write.setdefault(nm, i)
-            last_use[nm] = max(last_use.get(nm, i), i)
+            touch(v.buffer, i, True)
         for v in k.reads():
-            nm = v.buffer.name
-            by_name.setdefault(nm, v.buffer)
-            last_use[nm] = max(last_use.get(nm, i), i)
-    horizon = len(schedule.kernels)
-    for v in graph.outputs:
-        last_use[v.buffer.name] = horizon
+            touch(v.buffer, i, False)
+    for v in graph.outputs:  # results outlive the schedule
         by_name.setdefault(v.buffer.name, v.buffer)
+        last[v.buffer.name] = len(schedule.kernels)
 
-    ranges: list[LiveRange] = []
-    for nm, buf in by_name.items():
-        if not buf.plannable or nm not in first_write:
-            continue
-        start = first_write[nm]
-        ranges.append(LiveRange(buf, start, last_use.get(nm, start), _align(buf.nbytes)))
-    return ranges
+    return [LiveRange(buf, first[name], last[name], _round_up(buf.nbytes))
+            for name, buf in by_name.items() if buf.plannable and name in first]
 
 
 def peak_live_bytes(ranges: list[LiveRange], n_kernels: int) -> int:
-    if not ranges:
-        return 0
-    events = sorted([(r.start, r.size) for r in ranges] + [(r.end + 1, -r.size) for r in ranges])
-    live = peak = 0
-    for _, delta in events:
-        live += delta
-        peak = max(peak, live)
-    return peak
+    """Most bytes live at one kernel index (a lower bound on the arena)."""
+    delta: dict[int, int] = defaultdict(int)
+    for r in ranges:
+        delta[r.start] += r.size
+        delta[r.end + 1] -= r.size
+    return max(accumulate(delta[t] for t in sorted(delta)), default=0) if ranges else 0
+
+
+# --------------------------------------------------------------------------
+# placement
+# --------------------------------------------------------------------------
+
+def _lowest_fit(busy: list[tuple[int, int]], size: int) -> int:
+    """Lowest offset with ``size`` free bytes below the next busy extent;
+    ``busy`` are ``[lo, hi)`` byte extents (overlapping allowed)."""
+    at = 0
+    for lo, hi in sorted(busy):
+        if lo - at >= size:
+            break
+        at = max(at, hi)
+    return at
 
 
 def pack(ranges: list[LiveRange]) -> tuple[dict[str, int], int]:
-    """Greedy largest-first, lowest-fit placement."""
-    placed: list[tuple[int, LiveRange]] = []
+    """Offsets of every range and the arena size they need."""
+    order = sorted(ranges, key=lambda r: (-r.size, r.start, r.buffer.name))
     offsets: dict[str, int] = {}
+    placed: list[tuple[LiveRange, int]] = []
     arena = 0
-    for r in sorted(ranges, key=lambda r: (-r.size, r.start, r.buffer.name)):
-        blockers = sorted(((off, p) for off, p in placed if p.overlaps(r)), key=lambda t: t[0])
-        at = 0
-        for off, p in blockers:
-            if off >= at + r.size:
-                break
-            at = max(at, _align(off + p.size))
-        offsets[r.buffer.name] = at
-        placed.append((at, r))
-        arena = max(arena, at + r.size)
+    for r in order:
+        busy = [(off, _round_up(off + p.size)) for p, off in placed if p.overlaps(r)]
+        off = _lowest_fit(busy, r.size)
+        offsets[r.buffer.name] = off
+        placed.append((r, off))
+        arena = max(arena, off + r.size)
     return offsets, arena
 
 
 def verify(ranges: list[LiveRange], offsets: dict[str, int]) -> list[str]:
-    """Every pair of simultaneously live buffers must be byte-disjoint."""
-    problems: list[str] = []
-    for i, a in enumerate(ranges):
-        oa = offsets[a.buffer.name]
-        for b in ranges[i + 1:]:
-            if not a.overlaps(b):
-                continue
-            ob = offsets[b.buffer.name]
-            if oa < ob + b.size and ob < oa + a.size:
-                problems.append(
-                    f"{a.buffer.name}[{oa}:{oa + a.size}] live [{a.start},{a.end}] overlaps "
-                    f"{b.buffer.name}[{ob}:{ob + b.size}] live [{b.start},{b.end}]")
-    return problems
+    """Every pair of buffers live at one time that share a byte, described.
+    Two lifetimes overlap exactly when both are live at the later start, so
+    the check runs once per distinct start time over the buffers live then."""
+    found: list[str] = []
+    reported: set[tuple[str, str]] = set()
+    for t in sorted({r.start for r in ranges}):
+        live = sorted(((offsets[r.buffer.name], r) for r in ranges if r.start <= t <= r.end),
+                      key=lambda e: e[0])
+        for i, (off_a, a) in enumerate(live):
+            for off_b, b in live[i + 1:]:
+                if off_b >= off_a + a.size:
+                    break
+                if off_a >= off_b + b.size:  # b is empty and sits at a's start
+                    continue
+                pair = tuple(sorted((a.buffer.name, b.buffer.name)))
+                if pair in reported:
+                    continue
+                reported.add(pair)
+                found.append(f"{a.buffer.name} bytes [{off_a}, {off_a + a.size}) kernels "
+                             f"[{a.start}, {a.end}] share memory with {b.buffer.name} bytes "
+                             f"[{off_b}, {off_b + b.size}) kernels [{b.start}, {b.end}]")
+    return found
 
 
 def plan_memory(graph: Graph, schedule: Schedule, cfg: Config) -> AllocationPlan:
+    """Place (or, with ``memory_planning`` off, schedule the allocation of)
+    every intermediate; records the plan on ``schedule`` and each buffer."""
     ranges = compute_live_ranges(graph, schedule)
-    peak = peak_live_bytes(ranges, len(schedule.kernels))
-    total = sum(r.size for r in ranges)
-    by_name = {r.buffer.name: r for r in ranges}
-
-    if not cfg.memory_planning:
-        plan = AllocationPlan(mode="eager", peak_bytes=peak, total_bytes=total, live_ranges=by_name)
+    plan = AllocationPlan(mode="arena" if cfg.memory_planning else "eager",
+                          live_ranges={r.buffer.name: r for r in ranges},
+                          peak_bytes=peak_live_bytes(ranges, len(schedule.kernels)),
+                          total_bytes=sum(r.size for r in ranges))
+    if plan.mode == "eager":
         for r in ranges:
             plan.alloc_at.setdefault(r.start, []).append(r.buffer)
             if r.end < len(schedule.kernels):
                 plan.free_at.setdefault(r.end, []).append(r.buffer.name)
-        for b in graph.buffers():
-            b.arena_offset = None
-        schedule.arena_bytes = 0
-        schedule.plan = plan
-        return plan
-
-    offsets, arena = pack(ranges)
-    problems = verify(ranges, offsets)
-    if problems:
-        raise AssertionError("memory planner produced overlapping buffers:\n" + "\n".join(problems))
+    else:
+        plan.offsets, plan.arena_bytes = pack(ranges)
+        clashes = verify(ranges, plan.offsets)
+        if clashes:
+            raise AssertionError("arena placement overlaps live buffers:\n" + "\n".join(clashes))
     for b in graph.buffers():
-        b.arena_offset = offsets.get(b.name)
-    plan = AllocationPlan(mode="arena", arena_bytes=arena, offsets=offsets, live_ranges=by_name,
-                          peak_bytes=peak, total_bytes=total)
-    schedule.arena_bytes = arena
+        b.arena_offset = plan.offsets.get(b.name)
+    schedule.arena_bytes = plan.arena_bytes
     schedule.plan = plan
     return plan
