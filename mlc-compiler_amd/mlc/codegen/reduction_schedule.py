@@ -1,13 +1,20 @@
-"""Passes over the row of a reduction kernel.
+"""Passes over the row: how a reduction kernel's steps are traversed.
 
-A persistent kernel makes one pass (load the row, run every step, store). A
-streamed kernel (row longer than ``max_persistent_row``) makes one pass per
-reduction plus a final pass for the element-space stores, except that a max
-followed by ``sum(exp(x - max))`` collapses into one online-softmax pass:
+A *persistent* kernel holds its row: one pass loads it, runs every step and
+stores. A *streamed* kernel (rows longer than ``max_persistent_row``)
+cannot, so each reduction gets a pass of its own over memory, in step order,
+and a last pass computes and stores the element outputs. A pass re-evaluates
+only the binds it needs that vary along the columns; binds that read only
+row values (reduction results, per-row operands) are scalars computed once
+(``scalar_binds``).
 
-    m' = max(m, max(chunk));  l' = l * exp(m - m') + sum(exp(chunk - m'))
-
-Reference behaviour followed: ``mlc/codegen/reduction_schedule.py:23-219``.
+One pattern collapses two streamed passes into one: a max reduction followed
+by a sum of ``exp(x - max)`` of the same ``x`` (softmax). The running
+recurrence ``m' = max(m, x)``, ``l' = l * exp(m - m') + exp(x - m')`` yields
+both in one pass, every exponent still non-positive
+(:class:`OnlineSoftmax`). The HIP streamed template and the test oracle both
+follow this partition (reference counterpart:
+``mlc/codegen/reduction_schedule.py:119-219``).
 """
 
 from __future__ import annotations
@@ -22,131 +29,112 @@ from ..kernels import Bind, Reduce, ReductionKernel
 class OnlineSoftmax:
     max_step: Reduce
     sum_step: Reduce
-    #: the expression being maxed, whose shift the sum exponentiates
+    #: the expression maxed over (its shift is exponentiated and summed)
     value: Expr
 
 
 @dataclass
 class Pass:
-    """One traversal of the row: column-varying binds to recompute, the
-    accumulators updated, and the element outputs stored."""
-
+    #: column-varying binds evaluated in this pass, in step order
     binds: list[Bind] = field(default_factory=list)
+    #: reductions accumulated in this pass (two for an online softmax)
     reduces: list[Reduce] = field(default_factory=list)
+    #: element outputs stored in this pass
     stores: list[str] = field(default_factory=list)
     online_softmax: OnlineSoftmax | None = None
 
 
 def dependencies(steps: list) -> dict[str, set[str]]:
-    """step name -> the steps it needs, not looking past a reduce (whose
-    result is a scalar that survives between passes)."""
-    by_name = {s.name: s for s in steps}
-    memo: dict[str, set[str]] = {}
-
-    def need(name: str) -> set[str]:
-        if name in memo:
-            return memo[name]
-        memo[name] = set()
+    """Step name -> every step it needs, through binds; a reduction it reads is
+    included but not looked behind (its result outlives the pass that made
+    it, so nothing feeding it is evaluated again)."""
+    kind = {s.name: s for s in steps}
+    needs: dict[str, set[str]] = {}
+    for s in steps:  # steps only read earlier steps, so one forward sweep does
         found: set[str] = set()
-        step = by_name.get(name)
-        if step is not None:
-            for r in refs(step.expr):
-                found.add(r)
-                if not isinstance(by_name.get(r), Reduce):
-                    found |= need(r)
-        memo[name] = found
-        return found
-
-    return {s.name: need(s.name) for s in steps}
+        for r in refs(s.expr):
+            found.add(r)
+            if not isinstance(kind.get(r), Reduce):
+                found |= needs.get(r, set())
+        needs[s.name] = found
+    return needs
 
 
 def varies_by_column(kernel: ReductionKernel) -> set[str]:
-    """Bind steps that are vectors over the column axis."""
-    col_slots = {i for i, a in enumerate(kernel.inputs) if a.index.varies_along("col")}
-    vec: set[str] = set()
+    """Names of the binds whose value differs from column to column."""
+    column_slots = {i for i, a in enumerate(kernel.inputs) if a.index.varies_along("col")}
+    vector: set[str] = set()
     for s in kernel.steps:
-        if isinstance(s, Reduce):
-            continue
-        slots = {x.slot for x in walk(s.expr) if isinstance(x, Load)}
-        if slots & col_slots or refs(s.expr) & vec:
-            vec.add(s.name)
-    return vec
+        if isinstance(s, Bind):
+            slots = {x.slot for x in walk(s.expr) if isinstance(x, Load)}
+            if slots & column_slots or refs(s.expr) & vector:
+                vector.add(s.name)
+    return vector
+
+
+def scalar_binds(kernel: ReductionKernel) -> list[Bind]:
+    """Binds that are one value per row (hoisted out of any column loop)."""
+    vector = varies_by_column(kernel)
+    return [s for s in kernel.steps if isinstance(s, Bind) and s.name not in vector]
 
 
 def detect_online_softmax(kernel: ReductionKernel) -> OnlineSoftmax | None:
-    """Exactly two reduces: a max, then a sum of ``exp(x - max)`` of the same x."""
-    reds = kernel.reduces
-    if len(reds) != 2 or reds[0].kind != "max" or reds[1].kind != "sum":
+    """The kernel's two reductions as a max and a sum of ``exp(x - max)``
+    over the same ``x``, or None."""
+    reduces = kernel.reduces
+    if [r.kind for r in reduces] != ["max", "sum"]:
         return None
-    first, second = reds
-    by_name = {s.name: s for s in kernel.steps}
+    peak, total = reduces
+    binds = {s.name: s.expr for s in kernel.steps if isinstance(s, Bind)}
 
-    def through_binds(e: Expr) -> Expr:
-        while isinstance(e, Ref) and isinstance(by_name.get(e.name), Bind):
-            e = by_name[e.name].expr
+    def unfold(e: Expr) -> Expr:
+        while isinstance(e, Ref) and e.name in binds:
+            e = binds[e.name]
         return e
 
-    body = through_binds(second.expr)
-    if not (isinstance(body, Call) and body.fn == "exp"):
-        return None
-    inner = through_binds(body.args[0])
-    if not (isinstance(inner, Call) and inner.fn == "sub"):
-        return None
-    shifted, sub = through_binds(inner.args[0]), inner.args[1]
-    if not (isinstance(sub, Ref) and sub.name == first.name):
-        return None
-    if shifted != through_binds(first.expr):
-        return None
-    return OnlineSoftmax(first, second, first.expr)
+    def call_of(e: Expr, fn: str) -> Call | None:
+        e = unfold(e)
+        return e if isinstance(e, Call) and e.fn == fn else None
 
-
-def _in_order(steps: list, names: set[str]) -> list[str]:
-    return [s.name for s in steps if s.name in names]
+    exp = call_of(total.expr, "exp")
+    shift = call_of(exp.args[0], "sub") if exp is not None else None
+    if shift is None or shift.args[1] != Ref(peak.name):
+        return None
+    if unfold(shift.args[0]) != unfold(peak.expr):
+        return None
+    return OnlineSoftmax(peak, total, peak.expr)
 
 
 def plan_passes(kernel: ReductionKernel) -> list[Pass]:
-    element_stores = [a.value.name for a in kernel.outputs
-                      if a.value.name not in kernel.row_outputs]
+    """The passes over the row, in the order they run."""
+    element_stores = [a.value.name for a in kernel.outputs if a.value.name not in kernel.row_outputs]
     if not kernel.two_pass:
         return [Pass(binds=[s for s in kernel.steps if isinstance(s, Bind)],
                      reduces=kernel.reduces, stores=element_stores)]
 
-    deps = dependencies(kernel.steps)
+    needs = dependencies(kernel.steps)
     vector = varies_by_column(kernel)
-    by_name = {s.name: s for s in kernel.steps}
-    online = detect_online_softmax(kernel)
 
     def vector_binds(names: set[str]) -> list[Bind]:
-        return [by_name[n] for n in _in_order(kernel.steps, names)
-                if isinstance(by_name[n], Bind) and n in vector]
+        return [s for s in kernel.steps
+                if s.name in names and isinstance(s, Bind) and s.name in vector]
 
+    online = detect_online_softmax(kernel)
     passes: list[Pass] = []
-    reds = kernel.reduces
-    i = 0
-    while i < len(reds):
-        r = reds[i]
+    for r in kernel.reduces:
+        if online is not None and r is online.sum_step:
+            continue  # accumulated with the max by the recurrence
         if online is not None and r is online.max_step:
-            # the subtract and exp between the two reduces are subsumed by the
-            # recurrence; only what the maxed expression needs is recomputed
-            passes.append(Pass(binds=vector_binds(deps[r.name]),
-                               reduces=[online.max_step, online.sum_step],
+            # only what the maxed value needs: the shift and exponential
+            # between the two reductions are the recurrence's own work
+            passes.append(Pass(binds=vector_binds(needs[r.name]), reduces=[r, online.sum_step],
                                online_softmax=online))
-            i += 2
-            continue
-        passes.append(Pass(binds=vector_binds(deps[r.name] | {r.name}), reduces=[r]))
-        i += 1
-
+        else:
+            passes.append(Pass(binds=vector_binds(needs[r.name] | {r.name}), reduces=[r]))
     if element_stores:
-        needed: set[str] = set()
-        for nm in element_stores:
-            for ref in refs(kernel.out_expr[nm]):
-                needed.add(ref)
-                needed |= deps.get(ref, set())
-        passes.append(Pass(binds=vector_binds(needed), stores=element_stores))
+        wanted: set[str] = set()
+        for name in element_stores:
+            for ref in refs(kernel.out_expr[name]):
+                wanted |= {ref} | needs.get(ref, set())
+        passes.append(Pass(binds=vector_binds(wanted), stores=element_stores))
     return passes
-
-
-def scalar_binds(kernel: ReductionKernel) -> list[Bind]:
-    """Bind steps constant along the row (hoisted out of streaming loops)."""
-    vector = varies_by_column(kernel)
-    return [s for s in kernel.steps if isinstance(s, Bind) and s.name not in vector]

@@ -1,14 +1,27 @@
 """Fusion groups -> kernel IR.
 
-Each pointwise group becomes an iteration space, operands with index maps, a
-body of scalar expressions and a store list. A read of a value produced in
-the same kernel becomes a register reference exactly when its index map
-equals the one the value was produced at (canonical maps make that an
-equality test that sees through reshapes); otherwise it is a load.
+``build_schedule`` turns each group into one kernel: a pointwise group into a
+:class:`PointwiseKernel`, a reduction group into a :class:`ReductionKernel`
+(``codegen/reduction_lowering.py``), anything else -- matmuls, opaque ops,
+reductions with the pass off -- into an :class:`ExternKernel` library call.
 
-Reference behaviour followed: ``mlc/lower.py:40-292``: store set, read/write
-index maps, the register-reuse rule, operand slot order and input pruning,
-all of which fix the operand lists and index strings the backends see.
+Both generated kinds are assembled the same way (:class:`KernelAssembler`):
+walk the group's nodes in program order, lower each through the op
+registry's rule, and resolve every tensor operand to an *index map* over the
+kernel's iteration variables. An operand that an earlier member computed at
+the same map is taken from that member's register; otherwise it becomes a
+load slot (one slot per distinct buffer, dtype and map). Because index maps
+are canonical, a ``[B*T, D]`` GEMM output and the ``[B, T, D]`` view the next
+op reads are the same map, so the pair fuses without the value reaching
+memory. At the end, slots nothing reads are dropped and the rest renumbered.
+
+A value is stored when the graph returns it or some kernel that does not
+compute it reads it (``_values_to_store``; after recompute a node can be in
+several kernels, so this is decided over the whole schedule).
+
+Temp naming, slot order and the pruning rule give the reference's kernel IR
+for the same groups (``mlc/lower.py:40-292``), which the golden schedules
+check.
 """
 
 from __future__ import annotations
@@ -17,12 +30,10 @@ from .codegen.index import IndexMap, flat_index
 from .config import Config
 from .ir.graph import Graph, Node, Value
 from .ir.ops import _S, lookup
-from .ir.scalar import Const, Expr, Load, Ref
-from .ir.scalar import loads as expr_loads
-from .ir.scalar import substitute
-from .kernels import ExternKernel, Kernel, KernelArg, PointwiseKernel, Schedule
-from .passes.fusion import KernelGroup, _fits_space, group_space
-from .passes.scheduler import UseInfo, source_value
+from .ir.scalar import Const, Expr, Load, Ref, loads, substitute
+from .kernels import ExternKernel, KernelArg, PointwiseKernel, Schedule
+from .passes.fusion import BROADCAST, FULL, KernelGroup, _fits_space, group_space
+from .passes.grouping import UseInfo, source_value
 
 
 class LoweringError(Exception):
@@ -30,183 +41,184 @@ class LoweringError(Exception):
 
 
 def build_schedule(graph: Graph, groups: list[KernelGroup], cfg: Config) -> Schedule:
-    uses = UseInfo(graph)
-    stores = _store_set(graph, groups, uses)
-    kernels: list[Kernel] = []
+    stores = _values_to_store(groups, UseInfo(graph))
+    kernels = []
     for i, group in enumerate(groups):
-        name = f"k{i}"
-        kind = group.kind
+        name, kind = f"k{i}", group.kind
         if kind == "pointwise":
             kernels.append(build_pointwise(graph, group, stores, name))
         elif kind == "reduction" and cfg.reduction_fusion:
             from .codegen.reduction_lowering import build_reduction
 
             kernels.append(build_reduction(graph, group, stores, name, cfg))
-        else:
-            if len(group.nodes) != 1:
-                raise LoweringError(f"group of {len(group.nodes)} nodes has no kernel form: "
-                                    f"{[n.op for n in group.nodes]}")
+        elif len(group.nodes) == 1:
             node = group.nodes[0]
             kernels.append(ExternKernel(name, node, node.unique_tensor_args(), list(node.outputs)))
+        else:
+            raise LoweringError(f"{len(group.nodes)} nodes grouped into one library call: "
+                                f"{[n.op for n in group.nodes]}")
     return Schedule(graph, kernels)
 
 
-def _store_set(graph: Graph, groups: list[KernelGroup], uses: UseInfo) -> set[int]:
-    """ids of values that must reach memory: graph outputs, and values read by
-    some kernel that does not compute them itself."""
-    kernels_of: dict[int, set[int]] = {}
+def _values_to_store(groups: list[KernelGroup], uses: UseInfo) -> set[int]:
+    """ids of values that reach memory: graph outputs, and values some node
+    reads in a kernel that does not compute them."""
+    homes: dict[int, set[int]] = {}
     for gi, g in enumerate(groups):
         for n in g.nodes:
-            kernels_of.setdefault(id(n), set()).add(gi)
-    need: set[int] = set()
-    empty: set[int] = set()
-    for g in groups:
-        for n in g.nodes:
-            mine = kernels_of.get(id(n), empty)
-            for o in n.outputs:
-                if uses.escapes(o):
-                    need.add(id(o))
-                    continue
-                if any(not kernels_of.get(c, empty) <= mine for c in uses.consumers(o)):
-                    need.add(id(o))
-    return need
+            homes.setdefault(id(n), set()).add(gi)
+    stored = set()
+    for n in {id(n): n for g in groups for n in g.nodes}.values():
+        here = homes[id(n)]
+        for o in n.outputs:
+            if uses.escapes(o) or any(not homes.get(c, set()) <= here for c in uses.consumers(o)):
+                stored.add(id(o))
+    return stored
 
 
-def read_index(value: Value, consumer_shape: tuple[int, ...], space: tuple[int, ...]) -> IndexMap:
-    """Map at which a pointwise kernel reads ``value`` for a consumer whose
-    output has ``consumer_shape``."""
-    if _fits_space(consumer_shape, space) == "broadcast":
+# --------------------------------------------------------------------------
+# index maps of a pointwise kernel
+# --------------------------------------------------------------------------
+
+def read_index(value: Value, consumer_shape, space) -> IndexMap:
+    """The map a pointwise kernel over ``space`` reads ``value`` at, for a
+    node whose output has ``consumer_shape``: the operand broadcasts into the
+    node's shape, which broadcasts into (or reshapes to) the space."""
+    consumer_shape = tuple(consumer_shape)
+    if _fits_space(consumer_shape, space) == BROADCAST:
         return flat_index(space, value.layout.expand(consumer_shape).expand(space))
-    frame = tuple(consumer_shape)
-    lay = value.layout if tuple(value.shape) == frame else value.layout.expand(frame)
-    return flat_index(frame, lay)
+    if tuple(value.shape) == consumer_shape:
+        return flat_index(consumer_shape, value.layout)
+    return flat_index(consumer_shape, value.layout.expand(consumer_shape))
 
 
-def write_index(value: Value, space: tuple[int, ...]) -> IndexMap:
-    """Map at which ``value`` is held once computed in a kernel over ``space``."""
-    if _fits_space(value.shape, space) == "full":
+def write_index(value: Value, space) -> IndexMap:
+    """The map ``value`` is held at once a kernel over ``space`` computed it."""
+    if _fits_space(value.shape, space) == FULL:
         return flat_index(value.shape, value.layout)
     return flat_index(space, value.layout.expand(space))
 
 
-def reads_are_local(nodes, space: tuple[int, ...]) -> bool:
-    """True when every read of an in-kernel value hits the same index it was
-    produced at, so it can stay in the reading thread's registers."""
-    produced: dict[int, IndexMap] = {}
+def reads_are_local(nodes, space) -> bool:
+    """Each member reads every value another member computes at the map that
+    value is held at, so the read stays in the reading thread's registers.
+    (A bias add over ``[B*T, D]`` and a clone of a transposed view of it have
+    equal element counts, but iteration i would need iteration perm(i)'s
+    value: such a pair cannot share a pointwise kernel.)"""
+    held: dict[int, IndexMap] = {}
+    for o in (o for n in nodes for o in n.outputs):
+        if _fits_space(o.shape, space) is None:
+            return False
+        held[id(o)] = write_index(o, space)
     for n in nodes:
-        for o in n.outputs:
-            if _fits_space(o.shape, space) is None:
-                return False
-            produced[id(o)] = write_index(o, space)
-    for n in nodes:
-        shape = n.out.shape
-        for a in n.args:
-            if not isinstance(a, Value):
-                continue
-            at = produced.get(id(source_value(a)))
+        for a in (a for a in n.args if isinstance(a, Value)):
+            at = held.get(id(source_value(a)))
             if at is None:
                 continue
             try:
-                if read_index(a, shape, space) != at:
+                if read_index(a, n.out.shape, space) != at:
                     return False
             except ValueError:
                 return False
     return True
 
 
-def _prune_inputs(inputs: list[KernelArg], body, out_expr) -> list[KernelArg]:
-    """Drop operands nothing reads and renumber the remaining slots."""
-    used: set[int] = set()
-    for _, e in body:
-        used |= expr_loads(e)
-    for e in out_expr.values():
-        used |= expr_loads(e)
-    if len(used) == len(inputs):
-        return inputs
-    keep = sorted(used)
-    mapping = {Load(old): Load(new) for new, old in enumerate(keep)}
-    for i, (nm, e) in enumerate(body):
-        body[i] = (nm, substitute(e, mapping))
-    for k in list(out_expr):
-        out_expr[k] = substitute(out_expr[k], mapping)
-    return [inputs[i] for i in keep]
+# --------------------------------------------------------------------------
+# assembling a kernel
+# --------------------------------------------------------------------------
 
+class KernelAssembler:
+    """Operand slots, values held in registers and temp names of one kernel
+    under construction (subclassed per kernel kind)."""
 
-class _BodyBuilder:
-    def __init__(self, graph: Graph, nodes: list[Node]) -> None:
-        self.graph = graph
-        self.nodes = nodes
+    def __init__(self) -> None:
         self.inputs: list[KernelArg] = []
-        self._slots: dict[tuple, int] = {}
-        #: id(value) -> (expression holding it, index map it is held at)
-        self.env: dict[int, tuple[Expr, IndexMap]] = {}
-        self.body: list[tuple[str, Expr]] = []
-        self._temps = 0
+        self._slot_of: dict[tuple, int] = {}
+        #: id(value) -> (expression holding it, map it is held at)
+        self.held: dict[int, tuple[Expr, IndexMap]] = {}
+        self._serial = 0
 
-    def fresh(self) -> str:
-        name = f"t{self._temps}"
-        self._temps += 1
-        return name
+    def new_name(self, prefix: str = "t") -> str:
+        self._serial += 1
+        return f"{prefix}{self._serial - 1}"
 
     def load(self, v: Value, imap: IndexMap) -> Expr:
         key = (id(v.buffer), v.dtype, imap)
-        slot = self._slots.get(key)
-        if slot is None:
-            slot = self._slots[key] = len(self.inputs)
+        if key not in self._slot_of:
+            self._slot_of[key] = len(self.inputs)
             self.inputs.append(KernelArg(v, imap))
-        return Load(slot)
+        return Load(self._slot_of[key])
 
-    def operand(self, v: Value, imap: IndexMap) -> Expr:
-        live = self.env.get(id(source_value(v)))
-        if live is not None and live[1] == imap:
-            return live[0]
-        return self.load(v, imap)
+    def read(self, v: Value, imap: IndexMap) -> Expr:
+        """The register holding ``v`` at ``imap`` if there is one, else a load."""
+        held = self.held.get(id(source_value(v)))
+        return held[0] if held is not None and held[1] == imap else self.load(v, imap)
 
-    def emit(self, node: Node, arg_exprs: list) -> Expr:
-        """Lower one node; a bare load/ref/literal result gets no body line."""
+    @staticmethod
+    def lowered(node: Node, arg_exprs: list) -> Expr:
         spec = lookup(node.op)
         if spec is None or spec.lower is None:
-            raise LoweringError(f"no lowering rule for {node.op}")
-        expr = spec.lower(list(node.args), arg_exprs, dict(node.kwargs))
+            raise LoweringError(f"{node.op} has no scalar lowering rule")
+        return spec.lower(list(node.args), arg_exprs, dict(node.kwargs))
+
+    @staticmethod
+    def literal_or_passthrough(a):
+        """Non-tensor arguments: numbers become literals; dims, dtypes and the
+        like pass through for the lowering rule to read."""
+        return _S(a) if isinstance(a, (bool, int, float)) else a
+
+    def compact(self, exprs: list[Expr]) -> tuple[list[KernelArg], dict[Expr, Expr] | None]:
+        """Drop slots none of ``exprs`` reads: the kept operands, and the
+        renumbering to apply (None when every slot is read)."""
+        used = set().union(*map(loads, exprs)) if exprs else set()
+        if len(used) == len(self.inputs):
+            return self.inputs, None
+        kept = sorted(used)
+        return [self.inputs[i] for i in kept], {Load(old): Load(new) for new, old in enumerate(kept)}
+
+
+class _PointwiseAssembler(KernelAssembler):
+    def __init__(self) -> None:
+        super().__init__()
+        self.body: list[tuple[str, Expr]] = []
+
+    def bind(self, expr: Expr) -> Expr:
+        """One body line per real operation: a lowering that is a bare load,
+        register or literal (a clone, a no-op cast) binds nothing."""
         if isinstance(expr, (Load, Ref, Const)):
             return expr
-        name = self.fresh()
+        name = self.new_name()
         self.body.append((name, expr))
         return Ref(name)
 
 
 def build_pointwise(graph: Graph, group: KernelGroup, stores: set[int], name: str) -> PointwiseKernel:
     nodes = group.nodes
-    space = group_space(nodes)
-    b = _BodyBuilder(graph, nodes)
+    space = tuple(group_space(nodes))
+    asm = _PointwiseAssembler()
     for node in nodes:
         out = node.out
         if _fits_space(out.shape, space) is None:
-            raise LoweringError(f"{node.op} shape {out.shape} does not fit space {space}")
-        exprs: list = []
-        for a in node.args:
-            if isinstance(a, Value):
-                exprs.append(b.operand(a, read_index(a, out.shape, space)))
-            elif isinstance(a, (bool, int, float)):
-                exprs.append(_S(a))
-            else:
-                exprs.append(a)
-        b.env[id(out)] = (b.emit(node, exprs), write_index(out, space))
+            raise LoweringError(f"{node.op}{list(out.shape)} has no place in the space {space}")
+        args = [asm.read(a, read_index(a, out.shape, space)) if isinstance(a, Value)
+                else asm.literal_or_passthrough(a) for a in node.args]
+        asm.held[id(out)] = (asm.bind(asm.lowered(node, args)), write_index(out, space))
 
-    outputs: list[KernelArg] = []
-    out_expr: dict[str, Expr] = {}
+    outputs, out_expr = [], {}
     for node in nodes:
-        if id(node) not in group.owned:
-            continue
         out = node.out
-        if id(out) not in stores:
+        if id(node) not in group.owned or id(out) not in stores:
             continue
-        if _fits_space(out.shape, space) != "full":
-            raise LoweringError(f"{node.op} is broadcast inside its kernel but its result "
-                                "escapes; the fusion pass should not have grouped it")
+        if _fits_space(out.shape, space) != FULL:
+            raise LoweringError(f"{node.op}: a value evaluated per point of a larger space "
+                                "escapes its kernel")
         outputs.append(KernelArg(out, flat_index(out.shape, out.layout)))
-        out_expr[out.name] = b.env[id(out)][0]
+        out_expr[out.name] = asm.held[id(out)][0]
 
-    inputs = _prune_inputs(b.inputs, b.body, out_expr)
-    return PointwiseKernel(name=name, space=tuple(space), inputs=inputs, outputs=outputs,
-                           body=b.body, out_expr=out_expr, nodes=list(nodes))
+    inputs, renumber = asm.compact([e for _, e in asm.body] + list(out_expr.values()))
+    body = asm.body
+    if renumber is not None:
+        body = [(t, substitute(e, renumber)) for t, e in body]
+        out_expr = {k: substitute(e, renumber) for k, e in out_expr.items()}
+    return PointwiseKernel(name=name, space=space, inputs=inputs, outputs=outputs, body=body,
+                           out_expr=out_expr, nodes=list(nodes))

@@ -1,16 +1,27 @@
-"""Fusion planning: which nodes share a kernel.
+"""The fusion plan: which nodes share a kernel, in which order kernels run.
 
-Elementwise fusion grows maximal pointwise chains over one iteration space
-(an output that broadcasts into the space, or has the same element count as
-it, fits). A member whose output is smaller than the space is recomputed per
-point and so may not be visible outside the kernel (the escape rule). The
-cost model decides the rest. Reduction fusion then grows reduction groups,
-and recompute finally duplicates cheap multi-consumer producers.
+``plan`` runs three passes over one :class:`GroupGraph` partition:
 
-Reference behaviour followed: ``mlc/passes/fusion.py:32-381``, including the
-visiting order of the greedy loops and the tie-break in ``group_space``
-(first maximal output in the order the candidate list is given), since both
-decide which schedule comes out.
+1. **Elementwise** (``_Elementwise``): in program order, each pointwise node
+   tries to join the group of each pointwise producer it reads. A set of
+   nodes is *coherent* over the iteration space of its largest output when
+   every output either has the space's element count (a row-major reshape:
+   the flat index names the same element) or broadcasts into it. Outputs that
+   broadcast are re-evaluated at every point, so nothing outside the group
+   may need them (escape rule), and no member may read another's value at a
+   different index than it is held at (``lower.reads_are_local``). The merge
+   must then pay for itself in bytes (``grouping.evaluate_merge``): stores and
+   loads saved plus a launch, against re-evaluating work a group does over a
+   smaller space than the merged one.
+2. **Reductions** (``reduction_fusion.fuse_reductions``) grow reduction groups
+   over producers, siblings and consumers.
+3. **Recompute** (``_Recompute``), on the materialised groups: a cheap
+   pointwise group read by two or more other pointwise groups is copied into
+   each of them when that beats storing it once and loading it in each.
+
+The candidate orders, coherence and escape rules and prices reproduce the
+reference's elementwise and recompute passes (``mlc/passes/fusion.py:32-381``),
+because they decide the schedule, which is held bit-exact.
 """
 
 from __future__ import annotations
@@ -22,267 +33,244 @@ from ..config import Config
 from ..ir.graph import Graph, Node, Value
 from ..ir.ops import OpClass, is_pointwise, op_class
 from ..ir.shapes import ShapeError, broadcast_shapes
-from . import cost as costmod
-from .scheduler import GroupGraph, UseInfo, defining_node
+from .grouping import GroupGraph, UseInfo, defining_node, evaluate_merge, saved_traffic
 
+#: relations of an output shape to an iteration space (``_fits_space``)
+FULL, BROADCAST = "full", "broadcast"
 
-def _prod(shape) -> int:
-    return math.prod(shape) if shape else 1
+#: ops charged as expensive in the arithmetic term of the price
+_TRANSCENDENTAL = frozenset({"exp", "log", "erf", "tanh", "sigmoid", "pow", "sqrt", "rsqrt",
+                             "sin", "cos"})
 
 
 @dataclass
 class KernelGroup:
-    """Nodes destined for one kernel. ``owned`` are those this kernel stores;
-    nodes duplicated in by recompute are evaluated but not owned."""
+    """Nodes of one kernel. ``owned`` holds the ids of the nodes whose results
+    this kernel stores; a node copied in by recompute is evaluated for its
+    value only."""
 
     nodes: list[Node]
     owned: set[int] = field(default_factory=set)
 
     def __post_init__(self) -> None:
-        if not self.owned:
-            self.owned = {id(n) for n in self.nodes}
+        self.owned = self.owned or {id(n) for n in self.nodes}
 
     @property
     def kind(self) -> str:
         classes = {op_class(n.op) for n in self.nodes}
         if OpClass.REDUCTION in classes:
             return "reduction"
-        if classes == {OpClass.POINTWISE}:
-            return "pointwise"
-        return "extern"
+        return "pointwise" if classes == {OpClass.POINTWISE} else "extern"
 
     def space(self) -> tuple[int, ...]:
         return group_space(self.nodes)
 
 
 def group_space(nodes) -> tuple[int, ...]:
-    """The largest output shape among ``nodes`` (first one wins a tie)."""
-    best: tuple[int, ...] = ()
-    best_n = -1
-    for n in nodes:
-        for o in n.outputs:
-            if o.numel > best_n:
-                best, best_n = o.shape, o.numel
-    return best
+    """The shape of the output with the most elements (the earliest, in the
+    order given, among equals)."""
+    outs = [o for n in nodes for o in n.outputs]
+    if not outs:
+        return ()
+    most = max(o.numel for o in outs)
+    return next(o.shape for o in outs if o.numel == most)
 
 
 def _fits_space(shape: tuple[int, ...], space: tuple[int, ...]) -> str | None:
-    """'full' (same element count: a row-major reshape of the space),
-    'broadcast' (broadcasts into it) or None."""
-    ns, nsp = _prod(shape), _prod(space)
-    if ns == nsp:
-        return "full"
-    if ns > nsp:
-        return None
-    try:
-        return "broadcast" if broadcast_shapes([shape, space]) == space else None
-    except ShapeError:
-        return None
+    """``FULL`` (same element count), ``BROADCAST`` (broadcasts into
+    ``space``) or None (no place in it)."""
+    have, want = math.prod(shape), math.prod(space)
+    if have == want:
+        return FULL
+    if have < want:
+        try:
+            if broadcast_shapes([tuple(shape), tuple(space)]) == tuple(space):
+                return BROADCAST
+        except ShapeError:
+            pass
+    return None
 
 
-def _merged_space(nodes) -> tuple[int, ...] | None:
+def _coherent_space(nodes) -> tuple[int, ...] | None:
+    """The iteration space of ``nodes`` if every output fits it, else None."""
     space = group_space(nodes)
-    for n in nodes:
-        for o in n.outputs:
-            if _fits_space(o.shape, space) is None:
-                return None
-    return space
+    fits = all(_fits_space(o.shape, space) for n in nodes for o in n.outputs)
+    return space if fits else None
 
 
-def _escape_ok(nodes, space, uses: UseInfo, member_ids: set[int]) -> bool:
-    for n in nodes:
-        for o in n.outputs:
-            if _fits_space(o.shape, space) != "broadcast":
-                continue
-            if uses.escapes(o) or not uses.consumers(o) <= member_ids:
-                return False
-    return True
+def _no_broadcast_escapes(nodes, space, uses: UseInfo, allowed: set[int]) -> bool:
+    """Outputs evaluated per point of a larger space are read only by the
+    nodes in ``allowed`` and are not graph outputs."""
+    return all(not uses.escapes(o) and uses.consumers(o) <= allowed
+               for n in nodes for o in n.outputs if _fits_space(o.shape, space) == BROADCAST)
 
 
-_TRANSCENDENTAL = ("exp", "log", "erf", "tanh", "sigmoid", "pow", "sqrt", "rsqrt", "sin", "cos")
+def _ops_estimate(node: Node) -> int:
+    """Scalar operations of one node for the price: 12 for a transcendental,
+    2 otherwise."""
+    name = node.op.split(".")[-2] if "." in node.op else node.op
+    return 12 if name in _TRANSCENDENTAL else 2
 
 
-def _estimate_ops(node: Node) -> int:
-    tail = node.op.split(".")[-2] if "." in node.op else node.op
-    return 12 if tail in _TRANSCENDENTAL else 2
-
-
-def _reads_are_local(nodes, space) -> bool:
+def _register_local(nodes, space) -> bool:
     from ..lower import reads_are_local
 
     return reads_are_local(nodes, space)
 
 
-def _saved_traffic(a: list[Node], b: list[Node], uses: UseInfo, member_ids: set[int]):
-    """Values that stop round-tripping through memory if ``a`` and ``b`` merge."""
-    stores: list[Value] = []
-    loads: list[Value] = []
-    for group, other in ((a, b), (b, a)):
-        other_ids = {id(n) for n in other}
-        for n in group:
-            for o in n.outputs:
-                readers = uses.consumers(o)
-                if not (readers & other_ids):
-                    continue
-                loads.append(o)
-                if not uses.escapes(o) and readers <= member_ids:
-                    stores.append(o)
-    return stores, loads
-
-
-def _worth_merging(gg, gi, gj, space, uses, member_ids, cfg: Config) -> bool:
-    a = gg.group_members(gg.find(gi))
-    b = gg.group_members(gg.find(gj))
-    n_space = _prod(space)
-    stores, loads = _saved_traffic(a, b, uses, member_ids)
-    extra_evals = 0
-    expr_ops = 0
-    for group in (a, b):
-        n_group = _prod(group_space(group))
-        if n_group < n_space:
-            extra_evals += n_space - n_group
-            expr_ops = max(expr_ops, sum(_estimate_ops(n) for n in group))
-    return bool(costmod.evaluate_merge(cfg, saved_stores=stores, saved_loads=loads,
-                                       extra_loads=[], extra_evaluations=extra_evals,
-                                       expr_ops=expr_ops))
-
-
-def fuse_elementwise(graph: Graph, gg: GroupGraph, cfg: Config, uses: UseInfo) -> None:
-    """Greedy, in program order: pull each pointwise node's pointwise
-    producers into its group when every legality rule and the cost model agree."""
-    if not cfg.elementwise_fusion:
-        return
-    for node in gg.nodes:
-        if not is_pointwise(node.op):
-            continue
-        gi = gg.group_of(node)
-        for v in node.unique_tensor_args():
-            producer = defining_node(v)
-            if producer is None or not is_pointwise(producer.op):
-                continue
-            gj = gg.group_of(producer)
-            if gj is None or gg.find(gj) == gg.find(gi) or not gg.can_merge(gi, gj):
-                continue
-            merged = gg.group_members(gg.find(gi)) + gg.group_members(gg.find(gj))
-            space = _merged_space(merged)
-            if space is None:
-                continue
-            member_ids = {id(n) for n in merged}
-            if not _escape_ok(merged, space, uses, member_ids):
-                continue
-            if not _reads_are_local(merged, space):
-                continue
-            if not _worth_merging(gg, gi, gj, space, uses, member_ids, cfg):
-                continue
-            gi = gg.merge(gi, gj)
-
-
-# --------------------------------------------------------------------------
-# Recompute
-# --------------------------------------------------------------------------
-
-def apply_recompute(graph: Graph, groups: list[KernelGroup], cfg: Config,
-                    uses: UseInfo) -> list[KernelGroup]:
-    """Duplicate a cheap pointwise producer group into each of its (two or
-    more) consumer groups when that beats storing and reloading it."""
-    if not cfg.recompute:
-        return groups
-    while True:
-        owner = {id(n): gi for gi, g in enumerate(groups) for n in g.nodes if id(n) in g.owned}
-        fired = False
-        for gi, g in enumerate(groups):
-            if g.kind != "pointwise":
-                continue
-            produced = [o for n in g.nodes if id(n) in g.owned for o in n.outputs]
-            if any(uses.escapes(o) for o in produced):
-                continue
-            targets: set[int] = set()
-            for o in produced:
-                for cid in uses.consumers(o):
-                    cg = owner.get(cid)
-                    if cg is not None and cg != gi:
-                        targets.add(cg)
-            if len(targets) < 2:
-                continue
-            if not _recompute_legal(g, [groups[c] for c in targets], uses):
-                continue
-            if not _recompute_profitable(graph, groups, gi, targets, produced, cfg):
-                continue
-            for c in targets:
-                present = {id(x) for x in groups[c].nodes}
-                extra = [n for n in g.nodes if id(n) not in present]
-                groups[c].nodes = _sorted_nodes(graph, groups[c].nodes + extra)
-            groups = groups[:gi] + groups[gi + 1:]
-            fired = True
-            break
-        if not fired:
-            return groups
-
-
-def _recompute_legal(producer: KernelGroup, targets: list[KernelGroup], uses: UseInfo) -> bool:
-    """The merge rules per target, with the escape check made against all
-    targets together (after duplication each consumer holds its own copy)."""
-    if producer.kind != "pointwise" or any(t.kind != "pointwise" for t in targets):
-        return False
-    everyone = {id(n) for t in targets for n in t.nodes} | {id(n) for n in producer.nodes}
-    for t in targets:
-        merged = t.nodes + [n for n in producer.nodes if n not in t.nodes]
-        space = _merged_space(merged)
-        if space is None or not _escape_ok(merged, space, uses, everyone):
-            return False
-        if not _reads_are_local(merged, space):
-            return False
-    return True
-
-
-def _recompute_profitable(graph, groups, gi, targets, produced, cfg) -> bool:
-    g = groups[gi]
-    ops = sum(_estimate_ops(n) for n in g.nodes)
-    extra_evals = sum(_prod(groups[c].space()) for c in targets) - _prod(g.space())
-    already = {id(v.buffer) for c in targets for n in groups[c].nodes
-               for v in n.unique_tensor_args()}
-    extra_loads = [v for n in g.nodes for v in n.unique_tensor_args()
-                   if id(v.buffer) not in already]
-    return bool(costmod.evaluate_merge(cfg, saved_stores=produced,
-                                       saved_loads=produced * len(targets),
-                                       extra_loads=extra_loads, extra_evaluations=extra_evals,
-                                       expr_ops=ops, saved_launches=1))
-
-
-def _sorted_nodes(graph: Graph, nodes) -> list[Node]:
+def _in_program_order(graph: Graph, nodes) -> list[Node]:
     position = {id(n): i for i, n in enumerate(graph.nodes)}
-    out: list[Node] = []
-    seen: set[int] = set()
-    for n in sorted(nodes, key=lambda n: position[id(n)]):
-        if id(n) not in seen:
-            seen.add(id(n))
-            out.append(n)
-    return out
+    unique = {id(n): n for n in nodes}
+    return sorted(unique.values(), key=lambda n: position[id(n)])
 
+
+# --------------------------------------------------------------------------
+# elementwise
+# --------------------------------------------------------------------------
+
+class _Elementwise:
+    def __init__(self, gg: GroupGraph, cfg: Config, uses: UseInfo) -> None:
+        self.gg, self.cfg, self.uses = gg, cfg, uses
+
+    def run(self) -> None:
+        gg = self.gg
+        for node in gg.nodes:
+            if not is_pointwise(node.op):
+                continue
+            mine = gg.group_of(node)
+            for v in node.unique_tensor_args():
+                producer = defining_node(v)
+                if producer is None or not is_pointwise(producer.op):
+                    continue
+                theirs = gg.group_of(producer)
+                if theirs is not None and self._should_merge(mine, theirs):
+                    mine = gg.merge(mine, theirs)
+
+    def _should_merge(self, mine: int, theirs: int) -> bool:
+        gg = self.gg
+        if gg.find(mine) == gg.find(theirs) or not gg.can_merge(mine, theirs):
+            return False
+        a, b = gg.group_members(gg.find(mine)), gg.group_members(gg.find(theirs))
+        joined = a + b
+        space = _coherent_space(joined)
+        if space is None:
+            return False
+        ids = {id(n) for n in joined}
+        if not _no_broadcast_escapes(joined, space, self.uses, ids):
+            return False
+        return _register_local(joined, space) and self._pays(a, b, space, ids)
+
+    def _pays(self, a: list[Node], b: list[Node], space, ids: set[int]) -> bool:
+        stores, loads = saved_traffic(a, b, self.uses, ids)
+        size = math.prod(space)
+        repeats, ops = 0, 0
+        for part in (a, b):
+            own = math.prod(group_space(part))
+            if own < size:  # this part's work now runs at every point of the space
+                repeats += size - own
+                ops = max(ops, sum(map(_ops_estimate, part)))
+        return bool(evaluate_merge(self.cfg, saved_stores=stores, saved_loads=loads,
+                                   extra_loads=[], extra_evaluations=repeats, expr_ops=ops))
+
+
+# --------------------------------------------------------------------------
+# recompute
+# --------------------------------------------------------------------------
+
+class _Recompute:
+    """Copy a cheap pointwise group into each pointwise group reading it,
+    one group per round, until no group qualifies."""
+
+    def __init__(self, graph: Graph, cfg: Config, uses: UseInfo) -> None:
+        self.graph, self.cfg, self.uses = graph, cfg, uses
+
+    def run(self, groups: list[KernelGroup]) -> list[KernelGroup]:
+        while True:
+            owner = {id(n): gi for gi, g in enumerate(groups) for n in g.nodes if id(n) in g.owned}
+            chosen = next((gi for gi in range(len(groups))
+                           if self._inline_everywhere(groups, gi, owner)), None)
+            if chosen is None:
+                return groups
+            groups = groups[:chosen] + groups[chosen + 1:]
+
+    def _inline_everywhere(self, groups: list[KernelGroup], gi: int, owner: dict) -> bool:
+        """Inline group ``gi`` into all its reader groups if legal and
+        profitable; True when it did (the group is then dropped)."""
+        g = groups[gi]
+        if g.kind != "pointwise":
+            return False
+        produced = [o for n in g.nodes if id(n) in g.owned for o in n.outputs]
+        if any(self.uses.escapes(o) for o in produced):
+            return False
+        readers = {owner[c] for o in produced for c in self.uses.consumers(o)
+                   if owner.get(c, gi) != gi}
+        if len(readers) < 2:  # one reader: ordinary merging already decided
+            return False
+        targets = [groups[r] for r in readers]
+        if not self._legal(g, targets) or not self._pays(g, targets, produced):
+            return False
+        for t in targets:
+            present = {id(n) for n in t.nodes}
+            t.nodes = _in_program_order(self.graph, t.nodes + [n for n in g.nodes
+                                                               if id(n) not in present])
+        return True
+
+    def _legal(self, producer: KernelGroup, targets: list[KernelGroup]) -> bool:
+        # escape is judged against every copy at once: after inlining, a value
+        # read by two targets is held by both and has escaped nothing
+        if any(t.kind != "pointwise" for t in targets):
+            return False
+        everyone = {id(n) for g in (producer, *targets) for n in g.nodes}
+        for t in targets:
+            joined = t.nodes + [n for n in producer.nodes if n not in t.nodes]
+            space = _coherent_space(joined)
+            if space is None or not _no_broadcast_escapes(joined, space, self.uses, everyone):
+                return False
+            if not _register_local(joined, space):
+                return False
+        return True
+
+    def _pays(self, g: KernelGroup, targets: list[KernelGroup], produced: list[Value]) -> bool:
+        repeats = sum(math.prod(t.space()) for t in targets) - math.prod(g.space())
+        read = {id(v.buffer) for t in targets for n in t.nodes for v in n.unique_tensor_args()}
+        new_loads = [v for n in g.nodes for v in n.unique_tensor_args() if id(v.buffer) not in read]
+        return bool(evaluate_merge(self.cfg, saved_stores=produced,
+                                   saved_loads=produced * len(targets), extra_loads=new_loads,
+                                   extra_evaluations=repeats,
+                                   expr_ops=sum(map(_ops_estimate, g.nodes)), saved_launches=1))
+
+
+# --------------------------------------------------------------------------
+# the plan
+# --------------------------------------------------------------------------
 
 def plan(graph: Graph, cfg: Config) -> list[KernelGroup]:
-    """Elementwise fusion, then reduction fusion on the same group graph, then
-    recompute over the materialised groups; returns groups in schedule order."""
+    """Every fusion pass, then the kernel groups in execution order."""
     from .reduction_fusion import fuse_reductions
 
     uses = UseInfo(graph)
     gg = GroupGraph(graph)
-    fuse_elementwise(graph, gg, cfg, uses)
+    if cfg.elementwise_fusion:
+        _Elementwise(gg, cfg, uses).run()
     fuse_reductions(graph, gg, cfg, uses)
-    groups = [KernelGroup(_sorted_nodes(graph, gg.group_members(r))) for r in gg.roots_in_order()]
-    groups = apply_recompute(graph, groups, cfg, uses)
-    _validate(groups)
+    groups = [KernelGroup(_in_program_order(graph, gg.group_members(r)))
+              for r in gg.roots_in_order()]
+    if cfg.recompute:
+        groups = _Recompute(graph, cfg, uses).run(groups)
+    for g in groups:
+        _check_pointwise_group(g)
     return groups
 
 
-def _validate(groups: list[KernelGroup]) -> None:
-    for g in groups:
-        if g.kind != "pointwise":
-            continue
-        desc = ", ".join(f"{n.op}{list(n.out.shape)}" for n in g.nodes)
-        space = _merged_space(g.nodes)
-        if space is None:
-            raise AssertionError("fusion produced an incoherent group: " + desc)
-        if not _reads_are_local(g.nodes, space):
-            raise AssertionError("fusion produced a group where one member reads another "
-                                 "at a different index: " + desc)
+def _check_pointwise_group(g: KernelGroup) -> None:
+    """A pointwise group the passes produced must be coherent and read its
+    own values where they are held; anything else would miscompile."""
+    if g.kind != "pointwise":
+        return
+    listing = ", ".join(f"{n.op}{list(n.out.shape)}" for n in g.nodes)
+    space = _coherent_space(g.nodes)
+    if space is None:
+        raise AssertionError(f"fused group has no common iteration space: {listing}")
+    if not _register_local(g.nodes, space):
+        raise AssertionError("fused group reads one member's value at another member's index, "
+                             f"which no pointwise kernel expresses: {listing}")
