@@ -104,7 +104,7 @@ def _kernel_table(compiled, iters: int):
 
     from mlc.bench.roofline import algorithmic_bytes
     from mlc.kernels import ExternKernel
-    from mlc.runtime.executor import run_bound_extern
+    from mlc.runtime.executor import NativeCall, run_bound_extern
 
     rt = compiled._module
     stream = torch.cuda.current_stream().cuda_stream
@@ -112,7 +112,8 @@ def _kernel_table(compiled, iters: int):
     rows = []
     replayed = 0
     for i, (k, (kind, payload)) in enumerate(zip(compiled.schedule.kernels, plan)):
-        if isinstance(k, ExternKernel) and not (kind == "extern" and payload[0] == "native"):
+        native = kind == "extern" and isinstance(payload, NativeCall)
+        if isinstance(k, ExternKernel) and not native:
             continue
         for kind_j, payload_j in plan[replayed:i]:
             if kind_j == "extern":
@@ -120,7 +121,7 @@ def _kernel_table(compiled, iters: int):
             elif kind_j == "kernel":
                 rt.run_bound(payload_j)
         replayed = i
-        bound = payload if kind == "kernel" else payload[2]
+        bound = payload.bound if native else payload
         ms = rt.time_bound(bound, iters, stream)
         rows.append((k, rt.launch_table[k.name].symbol, algorithmic_bytes(k), ms))
     torch.cuda.synchronize()

@@ -1,162 +1,156 @@
-"""Workload definitions: BERT-base (post-norm encoder) and GPT-2 small
-(pre-norm causal decoder) in plain PyTorch, plus the single FFN block.
+"""The measured workloads as plain PyTorch modules (imports torch only).
 
-The architectures are the reference's benchmark models
-(``mlc/bench/models.py:87-224``) so export produces the same graph and the
-compiler the same schedule: post-norm BERT with an additive
-``(1 - mask) * finfo(fp32).min`` attention mask, erf-GELU and a tanh pooler;
-pre-norm GPT-2 with a ``finfo(fp32).min`` causal mask buffer. Weights are
-synthetic: ``build`` seeds 0 and, with ``init="normal"``, sets Linear and
-Embedding weights to N(0, 0.02), biases to 0, LayerNorm to (1, 0).
+From BASELINE.json's configurations:
+
+* BERT-base: a post-norm encoder -- word, position and token-type
+  embeddings summed and normalised; 12 layers of self-attention (separate q,
+  k, v projections, an additive padding mask of ``(1 - mask) * min(fp32)``)
+  and an erf-GELU MLP, each added back and LayerNorm'd (eps 1e-12); a tanh
+  pooler over the first token. Hidden 768, 12 heads, FFN 3072, vocabulary
+  30522, 512 positions.
+* GPT-2 small: a pre-norm decoder -- token and position embeddings; 12
+  blocks of causal self-attention (one fused qkv projection, an additive
+  ``min(fp32)`` upper-triangle mask) and an erf-GELU MLP around pre-norms
+  (eps 1e-5); a final norm and an untied vocabulary head. Hidden 768, 12
+  heads, vocabulary 50257, 1024 positions.
+* the FFN block of config 1: ``fc2(gelu_tanh(fc1(LayerNorm(x + r))))``.
+
+Small variants (4 layers, width 512, 8 heads, vocabulary 8192) keep tests
+fast. ``build`` seeds 0; ``init="normal"`` gives Linear and Embedding
+weights N(0, 0.02), biases 0 and LayerNorm (1, 0) as the configurations
+prescribe.
 """
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+FP32_MIN = torch.finfo(torch.float32).min
 
-@dataclass
-class BertConfig:
-    vocab_size: int = 30522
-    max_position: int = 512
-    n_layer: int = 12
-    n_head: int = 12
-    d_model: int = 768
-    d_ff: int = 3072
+
+@dataclass(frozen=True)
+class Shape:
+    """Sizes of one transformer stack."""
+
+    vocab: int
+    positions: int
+    layers: int = 12
+    heads: int = 12
+    width: int = 768
+    ffn: int = 3072
     eps: float = 1e-12
 
 
-@dataclass
-class GPTConfig:
-    vocab_size: int = 50257
-    block_size: int = 1024
-    n_layer: int = 12
-    n_head: int = 12
-    d_model: int = 768
-    eps: float = 1e-5
+class Attention(nn.Module):
+    """Multi-head self-attention over ``[B, T, width]`` with an additive mask
+    that broadcasts over ``[B, heads, T, T]``. ``fused`` keeps q, k and v in
+    one projection (GPT-2), otherwise three (BERT); the output projection is
+    the caller's."""
 
-
-class BertSelfAttention(nn.Module):
-    def __init__(self, cfg: BertConfig):
+    def __init__(self, s: Shape, fused: bool):
         super().__init__()
-        self.n_head = cfg.n_head
-        self.d_head = cfg.d_model // cfg.n_head
-        self.query = nn.Linear(cfg.d_model, cfg.d_model)
-        self.key = nn.Linear(cfg.d_model, cfg.d_model)
-        self.value = nn.Linear(cfg.d_model, cfg.d_model)
+        self.heads, self.head_width = s.heads, s.width // s.heads
+        if fused:
+            self.qkv = nn.Linear(s.width, 3 * s.width)
+        else:
+            self.q, self.k, self.v = (nn.Linear(s.width, s.width) for _ in range(3))
+        self.fused = fused
 
-    def _split_heads(self, x):
-        b, t, _ = x.shape
-        return x.view(b, t, self.n_head, self.d_head).transpose(1, 2)
+    def _per_head(self, t: torch.Tensor) -> torch.Tensor:
+        b, n, _ = t.shape
+        return t.view(b, n, self.heads, self.head_width).transpose(1, 2)
+
+    def forward(self, x: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        if self.fused:
+            q, k, v = self.qkv(x).chunk(3, dim=-1)
+        else:
+            q, k, v = self.q(x), self.k(x), self.v(x)
+        q, k, v = self._per_head(q), self._per_head(k), self._per_head(v)
+        scores = q @ k.transpose(-2, -1) / self.head_width ** 0.5 + mask
+        ctx = scores.softmax(dim=-1) @ v
+        b, _, n, _ = ctx.shape
+        return ctx.transpose(1, 2).reshape(b, n, -1)
+
+
+class EncoderLayer(nn.Module):
+    """Post-norm: ``norm(x + attn(x))`` then ``norm(x + mlp(x))``."""
+
+    def __init__(self, s: Shape):
+        super().__init__()
+        self.attn = Attention(s, fused=False)
+        self.attn_proj = nn.Linear(s.width, s.width)
+        self.attn_norm = nn.LayerNorm(s.width, eps=s.eps)
+        self.mlp_in = nn.Linear(s.width, s.ffn)
+        self.mlp_out = nn.Linear(s.ffn, s.width)
+        self.mlp_norm = nn.LayerNorm(s.width, eps=s.eps)
 
     def forward(self, x, mask):
-        q = self._split_heads(self.query(x))
-        k = self._split_heads(self.key(x))
-        v = self._split_heads(self.value(x))
-        scores = (q @ k.transpose(-2, -1)) / math.sqrt(self.d_head) + mask
-        probs = scores.softmax(dim=-1)
-        b, t, _ = x.shape
-        return (probs @ v).transpose(1, 2).reshape(b, t, -1)
+        x = self.attn_norm(x + self.attn_proj(self.attn(x, mask)))
+        return self.mlp_norm(x + self.mlp_out(F.gelu(self.mlp_in(x))))
 
 
-class BertLayer(nn.Module):
-    def __init__(self, cfg: BertConfig):
+class BertEncoder(nn.Module):
+    def __init__(self, s: Shape):
         super().__init__()
-        self.attn = BertSelfAttention(cfg)
-        self.attn_out = nn.Linear(cfg.d_model, cfg.d_model)
-        self.ln1 = nn.LayerNorm(cfg.d_model, eps=cfg.eps)
-        self.fc1 = nn.Linear(cfg.d_model, cfg.d_ff)
-        self.fc2 = nn.Linear(cfg.d_ff, cfg.d_model)
-        self.ln2 = nn.LayerNorm(cfg.d_model, eps=cfg.eps)
-
-    def forward(self, x, mask):
-        x = self.ln1(x + self.attn_out(self.attn(x, mask)))
-        return self.ln2(x + self.fc2(F.gelu(self.fc1(x))))
-
-
-class Bert(nn.Module):
-    def __init__(self, cfg: BertConfig = BertConfig()):
-        super().__init__()
-        self.cfg = cfg
-        self.word_emb = nn.Embedding(cfg.vocab_size, cfg.d_model)
-        self.pos_emb = nn.Embedding(cfg.max_position, cfg.d_model)
-        self.type_emb = nn.Embedding(2, cfg.d_model)
-        self.emb_ln = nn.LayerNorm(cfg.d_model, eps=cfg.eps)
-        self.layers = nn.ModuleList(BertLayer(cfg) for _ in range(cfg.n_layer))
-        self.pooler = nn.Linear(cfg.d_model, cfg.d_model)
-        self.register_buffer("positions", torch.arange(cfg.max_position), persistent=False)
+        self.tokens = nn.Embedding(s.vocab, s.width)
+        self.places = nn.Embedding(s.positions, s.width)
+        self.segments = nn.Embedding(2, s.width)
+        self.embed_norm = nn.LayerNorm(s.width, eps=s.eps)
+        self.layers = nn.ModuleList(EncoderLayer(s) for _ in range(s.layers))
+        self.pool = nn.Linear(s.width, s.width)
+        self.register_buffer("place_ids", torch.arange(s.positions), persistent=False)
 
     def forward(self, input_ids, attention_mask):
-        _, t = input_ids.shape
-        x = (self.word_emb(input_ids) + self.pos_emb(self.positions[:t])
-             + self.type_emb(torch.zeros_like(input_ids)))
-        x = self.emb_ln(x)
-        mask = (1.0 - attention_mask[:, None, None, :]) * torch.finfo(torch.float32).min
+        n = input_ids.shape[1]
+        segment_ids = torch.zeros_like(input_ids)  # one segment: token type 0
+        x = self.tokens(input_ids) + self.places(self.place_ids[:n]) + self.segments(segment_ids)
+        x = self.embed_norm(x)
+        mask = (1.0 - attention_mask[:, None, None, :]) * FP32_MIN
         for layer in self.layers:
             x = layer(x, mask)
-        return torch.tanh(self.pooler(x[:, 0]))
+        return torch.tanh(self.pool(x[:, 0]))
 
 
-class CausalSelfAttention(nn.Module):
-    def __init__(self, cfg: GPTConfig):
+class DecoderBlock(nn.Module):
+    """Pre-norm: ``x + attn(norm(x))`` then ``x + mlp(norm(x))``."""
+
+    def __init__(self, s: Shape):
         super().__init__()
-        self.n_head = cfg.n_head
-        self.d_head = cfg.d_model // cfg.n_head
-        self.qkv = nn.Linear(cfg.d_model, 3 * cfg.d_model)
-        self.proj = nn.Linear(cfg.d_model, cfg.d_model)
+        self.attn_norm = nn.LayerNorm(s.width, eps=s.eps)
+        self.attn = Attention(s, fused=True)
+        self.attn_proj = nn.Linear(s.width, s.width)
+        self.mlp_norm = nn.LayerNorm(s.width, eps=s.eps)
+        self.mlp_in = nn.Linear(s.width, s.ffn)
+        self.mlp_out = nn.Linear(s.ffn, s.width)
 
-    def forward(self, x, causal):
-        b, t, d = x.shape
-        q, k, v = self.qkv(x).chunk(3, dim=-1)
-        heads = (b, t, self.n_head, self.d_head)
-        q = q.view(heads).transpose(1, 2)
-        k = k.view(heads).transpose(1, 2)
-        v = v.view(heads).transpose(1, 2)
-        scores = (q @ k.transpose(-2, -1)) / math.sqrt(self.d_head) + causal[:, :, :t, :t]
-        probs = scores.softmax(dim=-1)
-        return self.proj((probs @ v).transpose(1, 2).reshape(b, t, d))
+    def forward(self, x, mask):
+        x = x + self.attn_proj(self.attn(self.attn_norm(x), mask))
+        return x + self.mlp_out(F.gelu(self.mlp_in(self.mlp_norm(x))))
 
 
-class GPTBlock(nn.Module):
-    def __init__(self, cfg: GPTConfig):
+class GPT2Decoder(nn.Module):
+    def __init__(self, s: Shape):
         super().__init__()
-        self.ln1 = nn.LayerNorm(cfg.d_model, eps=cfg.eps)
-        self.attn = CausalSelfAttention(cfg)
-        self.ln2 = nn.LayerNorm(cfg.d_model, eps=cfg.eps)
-        self.fc1 = nn.Linear(cfg.d_model, 4 * cfg.d_model)
-        self.fc2 = nn.Linear(4 * cfg.d_model, cfg.d_model)
-
-    def forward(self, x, causal):
-        x = x + self.attn(self.ln1(x), causal)
-        return x + self.fc2(F.gelu(self.fc1(self.ln2(x))))
-
-
-class GPT(nn.Module):
-    def __init__(self, cfg: GPTConfig = GPTConfig()):
-        super().__init__()
-        self.cfg = cfg
-        self.tok_emb = nn.Embedding(cfg.vocab_size, cfg.d_model)
-        self.pos_emb = nn.Embedding(cfg.block_size, cfg.d_model)
-        self.blocks = nn.ModuleList(GPTBlock(cfg) for _ in range(cfg.n_layer))
-        self.ln_f = nn.LayerNorm(cfg.d_model, eps=cfg.eps)
-        self.head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
-        tril = torch.tril(torch.ones(cfg.block_size, cfg.block_size))
-        causal = (1.0 - tril) * torch.finfo(torch.float32).min
-        self.register_buffer("causal", causal.view(1, 1, cfg.block_size, cfg.block_size),
-                             persistent=False)
-        self.register_buffer("positions", torch.arange(cfg.block_size), persistent=False)
+        self.tokens = nn.Embedding(s.vocab, s.width)
+        self.places = nn.Embedding(s.positions, s.width)
+        self.blocks = nn.ModuleList(DecoderBlock(s) for _ in range(s.layers))
+        self.final_norm = nn.LayerNorm(s.width, eps=s.eps)
+        self.lm_head = nn.Linear(s.width, s.vocab, bias=False)
+        future = torch.ones(s.positions, s.positions).triu(1) * FP32_MIN
+        self.register_buffer("future", future[None, None], persistent=False)
+        self.register_buffer("place_ids", torch.arange(s.positions), persistent=False)
 
     def forward(self, input_ids):
-        _, t = input_ids.shape
-        x = self.tok_emb(input_ids) + self.pos_emb(self.positions[:t])
+        n = input_ids.shape[1]
+        x = self.tokens(input_ids) + self.places(self.place_ids[:n])
+        mask = self.future[:, :, :n, :n]
         for block in self.blocks:
-            x = block(x, self.causal)
-        return self.head(self.ln_f(x))
+            x = block(x, mask)
+        return self.lm_head(self.final_norm(x))
 
 
 class FFNBlock(nn.Module):
@@ -172,26 +166,28 @@ class FFNBlock(nn.Module):
         return self.fc2(F.gelu(self.fc1(self.ln(x + r)), approximate="tanh"))
 
 
-def _bert_inputs(vocab):
+BERT_BASE = Shape(vocab=30522, positions=512)
+GPT2_SMALL = Shape(vocab=50257, positions=1024, eps=1e-5)
+_SMALL = dict(layers=4, heads=8, width=512, ffn=2048, vocab=8192)
+
+
+def _ids_and_mask(vocab):
     return lambda b, t, dev: (torch.randint(0, vocab, (b, t), device=dev),
                               torch.ones(b, t, device=dev))
 
 
-def _gpt_inputs(vocab):
+def _ids(vocab):
     return lambda b, t, dev: (torch.randint(0, vocab, (b, t), device=dev),)
 
 
-#: name -> (model builder, input builder, default sequence length)
+#: name -> (model factory, input factory, default sequence length)
 SUITE = {
-    "bert-base": (lambda: Bert(BertConfig()), _bert_inputs(30522), 128),
-    "bert-small": (lambda: Bert(BertConfig(n_layer=4, n_head=8, d_model=512, d_ff=2048,
-                                           vocab_size=8192)), _bert_inputs(8192), 128),
-    "gpt2-small": (lambda: GPT(GPTConfig()), _gpt_inputs(50257), 128),
-    "gpt-small": (lambda: GPT(GPTConfig(n_layer=4, n_head=8, d_model=512, vocab_size=8192,
-                                        block_size=256)), _gpt_inputs(8192), 128),
-    "ffn-block": (lambda: FFNBlock(),
-                  lambda b, t, dev: (torch.randn(b, t, 768, device=dev),
-                                     torch.randn(b, t, 768, device=dev)), 128),
+    "bert-base": (lambda: BertEncoder(BERT_BASE), _ids_and_mask(BERT_BASE.vocab), 128),
+    "bert-small": (lambda: BertEncoder(Shape(positions=512, **_SMALL)), _ids_and_mask(8192), 128),
+    "gpt2-small": (lambda: GPT2Decoder(GPT2_SMALL), _ids(GPT2_SMALL.vocab), 128),
+    "gpt-small": (lambda: GPT2Decoder(Shape(positions=256, eps=1e-5, **_SMALL)), _ids(8192), 128),
+    "ffn-block": (FFNBlock, lambda b, t, dev: (torch.randn(b, t, 768, device=dev),
+                                               torch.randn(b, t, 768, device=dev)), 128),
 }
 
 
@@ -199,13 +195,13 @@ def normal_init_(model: nn.Module, std: float = 0.02) -> nn.Module:
     """Linear/Embedding weights ~ N(0, std), biases 0, LayerNorm (1, 0)."""
     with torch.no_grad():
         for m in model.modules():
-            if isinstance(m, (nn.Linear, nn.Embedding)):
+            if isinstance(m, nn.LayerNorm):
+                nn.init.ones_(m.weight)
+                nn.init.zeros_(m.bias)
+            elif isinstance(m, (nn.Linear, nn.Embedding)):
                 m.weight.normal_(0.0, std)
                 if getattr(m, "bias", None) is not None:
-                    m.bias.zero_()
-            elif isinstance(m, nn.LayerNorm):
-                m.weight.fill_(1.0)
-                m.bias.zero_()
+                    nn.init.zeros_(m.bias)
     return model
 
 
@@ -217,19 +213,16 @@ def ffn_block_config1(seed: int = 0):
     with torch.no_grad():
         m.ln.weight.normal_(1.0, 0.02)
         m.ln.bias.normal_(0.0, 0.02)
-        m.fc1.weight.normal_(0.0, 0.02)
-        m.fc1.bias.zero_()
-        m.fc2.weight.normal_(0.0, 0.02)
-        m.fc2.bias.zero_()
-    x = torch.randn(1, 128, 768)
-    r = torch.randn(1, 128, 768)
-    return m, (x, r)
+        for fc in (m.fc1, m.fc2):
+            fc.weight.normal_(0.0, 0.02)
+            fc.bias.zero_()
+    return m, (torch.randn(1, 128, 768), torch.randn(1, 128, 768))
 
 
 def build(name: str, batch: int, seq: int | None = None, device: str | torch.device = "cpu",
           dtype: torch.dtype = torch.float32, init: str = "default"):
-    """Model and inputs, seeded 0. ``dtype`` halves weights and float inputs;
-    index tensors stay integral."""
+    """Model and inputs, seeded 0 (``init="normal"``: the N(0, 0.02) scheme).
+    A reduced ``dtype`` applies to weights and float inputs, not to ids."""
     make_model, make_inputs, default_seq = SUITE[name]
     torch.manual_seed(0)
     model = make_model().eval()

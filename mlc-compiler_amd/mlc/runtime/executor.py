@@ -1,22 +1,41 @@
-"""Runtime: the buffer table, the pre-resolved launch plan and graph replay.
+"""The compiled model: a fixed buffer table, a resolved launch plan, a graph.
 
-Every buffer is a flat 1-D tensor; shapes and strides live in the IR. Params
-are resident, inputs are copied into fixed buffers, intermediates are slices
-of the arena (one ``hipMalloc`` slab on the GPU), outputs alias storage the
-next call overwrites. The plan is resolved once; on the GPU consecutive
-generated kernels run as one native launch range and the whole schedule
-(generated kernels and extern library calls) is captured into one hipGraph.
+Calling a :class:`CompiledModel` copies the inputs into fixed device
+buffers and replays one captured hipGraph of the whole schedule (generated
+kernels through ``libmlc_hip.so``, library calls through torch), then hands
+back views of the output buffers.
 
-Reference behaviour followed: ``mlc/runtime/executor.py:28-474`` (buffer
-liveness, resident table, arena binding, extern ``.out`` dispatch decided from
-the schema, output aliasing, the eager alloc/free mode, 3 warm-up runs before
-capture, per-kernel profiling). The generated-kernel runner is pluggable so
-the test suite can execute the same plan with the CPU oracle; the product
-itself only ever selects the HIP runner and fails loudly without one.
+Memory (``_Buffers``):
+
+* params are uploaded once and stay resident, each a flat 1-D tensor;
+* planned intermediates are slices of the arena -- one ``hipMalloc`` slab, or
+  the library's static array -- at the planner's offsets, so every pointer a
+  kernel sees is the same on every call (what makes capture valid);
+* inputs are copied into buffers of their own each call, never aliased;
+* outputs alias storage the next call overwrites (clone to keep one).
+
+With ``memory_planning`` off the plan is "eager": intermediates are allocated
+just before the kernel that writes them and dropped after their last reader,
+and nothing is captured.
+
+Library calls (``ExternCall``) are resolved once against the buffer table:
+when the op has an ``.out`` overload taking exactly its arguments plus
+``out`` (read off the schemas, never by calling it) the result is written
+straight into its buffer; otherwise the op is called and its result copied.
+The HIP runtime may claim an op with a native kernel instead (``NativeCall``:
+the bounds-checked embedding gather).
+
+Behaviour kept from the reference runtime (``mlc/runtime/executor.py:41-474``):
+the input checks and their messages, output aliasing, the eager mode, three
+warm-up runs before capture, per-kernel profiling. The runner of generated
+kernels is pluggable so the tests can execute the same plan with the CPU
+oracle; the product only ever selects the HIP runtime and raises without a
+GPU.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Any, Sequence
 
 import torch
@@ -31,23 +50,215 @@ class ExecutionError(Exception):
 
 
 def select_backend(cfg: Config, device: torch.device) -> str:
+    """``"hip"``, for a ROCm GPU device (torch names it ``cuda``)."""
     if cfg.backend not in ("auto", "hip"):
-        raise ExecutionError(f"unknown backend {cfg.backend!r}; this build provides 'hip'")
+        raise ExecutionError(f"backend {cfg.backend!r} is not built here; this build runs 'hip'")
     if device.type != "cuda":
         raise ExecutionError(
-            f"the HIP backend runs on a ROCm GPU (torch device 'cuda'); got {device}. "
-            "CPU execution of the kernel IR is the parity oracle's job, not the product's")
+            f"the HIP backend runs on a ROCm GPU (torch device 'cuda'), not on {device}; "
+            "running the kernel IR on the CPU is the test oracle's job, not the product's")
     return "hip"
 
 
+# --------------------------------------------------------------------------
+# library calls
+# --------------------------------------------------------------------------
+
+def _materialise(a, buffers: dict[str, torch.Tensor]):
+    """Graph values inside an argument structure -> tensor views."""
+    if isinstance(a, Value):
+        return a.layout.as_torch(buffers[a.buffer.name])
+    if isinstance(a, (list, tuple)):
+        return type(a)(_materialise(x, buffers) for x in a)
+    return a
+
+
+def out_variant(node):
+    """The op's ``.out`` overload when its schema is the default overload's
+    arguments followed by ``out`` (cached in ``node.meta``), else None."""
+    if "out_variant" not in node.meta:
+        node.meta["out_variant"] = _find_out_overload(node)
+    return node.meta["out_variant"]
+
+
+def _find_out_overload(node):
+    target = node.meta.get("target")
+    if not node.op.startswith("aten.") or len(node.outputs) != 1 or not hasattr(target, "_schema"):
+        return None
+    packet = getattr(torch.ops.aten, node.op.split(".")[1], None)
+    candidate = getattr(packet, "out", None)
+    try:
+        default_args = [a.name for a in target._schema.arguments]
+        out_args = [a.name for a in candidate._schema.arguments]
+    except AttributeError:
+        return None
+    return candidate if out_args == default_args + ["out"] else None
+
+
+@dataclass
+class ExternCall:
+    """A torch op bound to the buffer table: run() writes its buffers."""
+
+    target: Any
+    overload: Any  # the .out overload, or None
+    args: list
+    kwargs: dict
+    dest: torch.Tensor | None
+    outs: list[torch.Tensor]
+
+    def run(self) -> None:
+        if self.overload is not None:
+            self.overload(*self.args, **self.kwargs, out=self.dest)
+            return
+        result = self.target(*self.args, **self.kwargs)
+        for buf, r in zip(self.outs, result if isinstance(result, (list, tuple)) else [result]):
+            buf.copy_(r.contiguous().reshape(-1))
+
+    def functional(self) -> "ExternCall":
+        return ExternCall(self.target, None, self.args, self.kwargs, None, self.outs)
+
+
+@dataclass
+class NativeCall:
+    """A library op the runtime implements with a kernel of its own."""
+
+    module: Any
+    bound: Any
+
+    def run(self) -> None:
+        self.module.run_bound(self.bound)
+
+
+def bind_extern(k: ExternKernel, buffers: dict[str, torch.Tensor], module=None):
+    """Resolve a library call against the buffer table without running it."""
+    claim = getattr(module, "bind_native_extern", None)
+    bound = claim(k, buffers) if claim is not None else None
+    if bound is not None:
+        return NativeCall(module, bound)
+    node = k.node
+    target = node.meta.get("target")
+    if target is None:
+        raise ExecutionError(f"{node.op}: no torch op to dispatch to")
+    overload = out_variant(node)
+    dest = None
+    if overload is not None:
+        out = node.outputs[0]
+        dest = out.layout.as_torch(buffers[out.buffer.name])
+    return ExternCall(target, overload, [_materialise(a, buffers) for a in node.args],
+                      {n: _materialise(v, buffers) for n, v in node.kwargs.items()}, dest,
+                      [buffers[o.buffer.name] for o in node.outputs])
+
+
+def run_bound_extern(call) -> None:
+    call.run()
+
+
+def run_extern(k: ExternKernel, buffers: dict[str, torch.Tensor], module=None) -> None:
+    """Bind and run one library call (the unplanned path). An ``.out``
+    overload that rejects this call is dropped for the node, which then runs
+    functionally and is copied into its buffer."""
+    call = bind_extern(k, buffers, module)
+    if isinstance(call, ExternCall) and call.overload is not None:
+        try:
+            call.run()
+            return
+        except (RuntimeError, TypeError):
+            k.node.meta["out_variant"] = None
+            call = call.functional()
+    call.run()
+
+
+# --------------------------------------------------------------------------
+# buffers
+# --------------------------------------------------------------------------
+
+class _Buffers:
+    """The model's device memory: resident params, fixed inputs, the arena."""
+
+    def __init__(self, model: "CompiledModel") -> None:
+        self.model = model
+        graph, schedule = model.graph, model.schedule
+        self.live = {v.buffer.name for v in (*graph.inputs, *graph.outputs)}
+        for k in schedule.kernels:
+            self.live.update(v.buffer.name for v in (*k.reads(), *k.writes()))
+        self.params = {v.buffer.name: graph.param_tensors[v.name].to(model.device).contiguous()
+                       .reshape(-1) for v in graph.params}
+        self.arena: torch.Tensor | None = None
+        self.table: dict[str, torch.Tensor] | None = None
+        self.inputs: list[torch.Tensor] = []
+
+    def empty(self, b) -> torch.Tensor:
+        return torch.empty(b.numel, dtype=b.dtype, device=self.model.device)
+
+    def _base(self) -> dict[str, torch.Tensor]:
+        """Resident params and every live buffer outside the arena's reach."""
+        table = {n: t for n, t in self.params.items() if n in self.live}
+        for b in self.model.graph.buffers():
+            if b.name not in table and not b.plannable and b.name in self.live:
+                table[b.name] = self.empty(b)
+        return table
+
+    def per_call(self, inputs: Sequence[torch.Tensor]) -> dict[str, torch.Tensor]:
+        """Eager mode: the caller's inputs used in place, intermediates come
+        and go with the alloc/free plan."""
+        table = self._base()
+        for v, t in zip(self.model.graph.inputs, inputs):
+            table[v.buffer.name] = t.to(self.model.device).contiguous().reshape(-1)
+        return table
+
+    def resident(self, inputs: Sequence[torch.Tensor]) -> dict[str, torch.Tensor]:
+        """The fixed table (built on first use) with this call's inputs
+        copied in."""
+        model = self.model
+        if self.table is None:
+            table = self._base()
+            for v in model.graph.inputs:
+                table[v.buffer.name] = torch.empty(v.buffer.numel, dtype=v.dtype,
+                                                   device=model.device)
+            for k in model.schedule.kernels:
+                if k.name in model._constants:
+                    for v in k.writes():
+                        table.setdefault(v.buffer.name, self.empty(v.buffer))
+            self._place_in_arena(table)
+            self.table = table
+            self.inputs = [table[v.buffer.name] for v in model.graph.inputs]
+        for dst, src in zip(self.inputs, inputs):
+            dst.copy_(src.reshape(-1), non_blocking=True)
+        return self.table
+
+    def _place_in_arena(self, table: dict[str, torch.Tensor]) -> None:
+        plan = self.model.schedule.plan
+        offsets = plan.offsets if plan is not None else {}
+        arena = self.get_arena()
+        for b in self.model.graph.buffers():
+            if b.name in table or b.name not in self.live:
+                continue
+            at = offsets.get(b.name)
+            table[b.name] = self.empty(b) if at is None else arena[at:at + b.nbytes].view(b.dtype)
+
+    def get_arena(self) -> torch.Tensor:
+        need = max(self.model.schedule.arena_bytes, 1)
+        if self.arena is None or self.arena.numel() < need:
+            make = getattr(self.model._module, "arena", None)
+            self.arena = make(need) if make is not None else torch.empty(
+                need, dtype=torch.uint8, device=self.model.device)
+        return self.arena
+
+
+# --------------------------------------------------------------------------
+# the model
+# --------------------------------------------------------------------------
+
+def _alloc_count(device) -> int:
+    return int(torch.cuda.memory_stats(device).get("allocation.all.allocated", 0))
+
+
 class CompiledModel:
-    """A compiled graph, callable like the module it came from."""
+    """A compiled graph, called like the module it came from."""
 
     def __init__(self, graph: Graph, schedule: Schedule, cfg: Config, device: torch.device,
                  runner: Any = None) -> None:
-        self.graph = graph
-        self.schedule = schedule
-        self.cfg = cfg
+        self.graph, self.schedule, self.cfg = graph, schedule, cfg
         self.device = torch.device(device)
         if runner is None:
             self.backend = select_backend(cfg, self.device)
@@ -55,176 +266,38 @@ class CompiledModel:
 
             self._module = HipRuntime(schedule, cfg, self.device)
         else:
-            self.backend = getattr(runner, "name", "custom")
-            self._module = runner
-
-        self.params: dict[str, torch.Tensor] = {}
-        for v in graph.params:
-            t = graph.param_tensors[v.name]
-            self.params[v.buffer.name] = t.to(self.device).contiguous().reshape(-1)
-
-        self._arena: torch.Tensor | None = None
-        self._live = self._live_buffers()
-        # externs reading no tensor (``aten.scalar_tensor``, ``full``, ...):
-        # their result never changes, so they run once when the plan is
-        # built, into memory of their own, and are not replayed. One that
-        # allocates (no ``out=`` form) would otherwise allocate inside the
-        # captured graph.
+            self.backend, self._module = getattr(runner, "name", "custom"), runner
+        # library calls reading no tensor always give the same result: they run
+        # once, into memory of their own, when the plan is resolved (one with
+        # no out= form would otherwise allocate inside the captured graph)
         self._constants = {k.name for k in schedule.kernels
                            if isinstance(k, ExternKernel) and not k.reads()}
-        self._resident: dict[str, torch.Tensor] | None = None
+        self._buffers = _Buffers(self)
         self._plan: list | None = None
         self._runs: list | None = None
-        self._static_inputs_flat: list[torch.Tensor] | None = None
         self._captured = False
         self._capture_stream = None
-        self._static_inputs: list[torch.Tensor] | None = None
         self._static_outputs: Any = None
 
-    # -- allocation -----------------------------------------------------------
-    def _live_buffers(self) -> set[str]:
-        live = {v.buffer.name for v in self.graph.inputs}
-        live |= {v.buffer.name for v in self.graph.outputs}
-        for k in self.schedule.kernels:
-            live |= {v.buffer.name for v in k.reads()}
-            live |= {v.buffer.name for v in k.writes()}
-        return live
+    # state the tests and the bench inspect
+    params = property(lambda self: self._buffers.params)
+    _arena = property(lambda self: self._buffers.arena)
+    _resident = property(lambda self: self._buffers.table)
 
+    # -- inputs and outputs ---------------------------------------------------
     def _check_inputs(self, inputs: Sequence[torch.Tensor]) -> None:
-        if len(inputs) != len(self.graph.inputs):
-            raise ExecutionError(f"expected {len(self.graph.inputs)} inputs, got {len(inputs)}")
-        for v, t in zip(self.graph.inputs, inputs):
+        expected = self.graph.inputs
+        if len(inputs) != len(expected):
+            raise ExecutionError(f"expected {len(expected)} inputs, got {len(inputs)}")
+        for v, t in zip(expected, inputs):
             if tuple(t.shape) != v.shape:
                 raise ExecutionError(
                     f"input {v.name}: compiled for {v.shape}, called with {tuple(t.shape)}")
 
-    def _empty(self, b) -> torch.Tensor:
-        return torch.empty(b.numel, dtype=b.dtype, device=self.device)
-
-    def _bind_resident(self, inputs: Sequence[torch.Tensor]) -> dict[str, torch.Tensor]:
-        """Unplanned mode: params, this call's inputs and the non-plannable
-        buffers (intermediates come and go per the alloc/free plan)."""
-        self._check_inputs(inputs)
-        buffers = {n: t for n, t in self.params.items() if n in self._live}
-        for v, t in zip(self.graph.inputs, inputs):
-            buffers[v.buffer.name] = t.to(self.device).contiguous().reshape(-1)
-        for b in self.graph.buffers():
-            if b.name in buffers or b.plannable or b.name not in self._live:
-                continue
-            buffers[b.name] = self._empty(b)
-        return buffers
-
-    def _get_arena(self) -> torch.Tensor:
-        need = max(self.schedule.arena_bytes, 1)
-        if self._arena is None or self._arena.numel() < need:
-            make = getattr(self._module, "arena", None)
-            if make is not None:
-                self._arena = make(need)
-            else:
-                self._arena = torch.empty(need, dtype=torch.uint8, device=self.device)
-        return self._arena
-
-    def _bind_arena(self, buffers: dict[str, torch.Tensor]) -> None:
-        plan = self.schedule.plan
-        arena = self._get_arena()
-        for b in self.graph.buffers():
-            if b.name in buffers or b.name not in self._live:
-                continue
-            offset = plan.offsets.get(b.name) if plan is not None else None
-            if offset is None:
-                buffers[b.name] = self._empty(b)
-            else:
-                buffers[b.name] = arena[offset:offset + b.nbytes].view(b.dtype)
-
-    def _resident_buffers(self, inputs: Sequence[torch.Tensor]) -> dict[str, torch.Tensor]:
-        """The buffer table, built once; inputs are copied into fixed buffers
-        so every pointer is stable for the life of the model."""
-        self._check_inputs(inputs)
-        if self._resident is None:
-            buffers = {n: t for n, t in self.params.items() if n in self._live}
-            for b in self.graph.buffers():
-                if b.name in buffers or b.plannable or b.name not in self._live:
-                    continue
-                buffers[b.name] = self._empty(b)
-            for v in self.graph.inputs:
-                buffers[v.buffer.name] = torch.empty(v.buffer.numel, dtype=v.dtype,
-                                                     device=self.device)
-            for k in self.schedule.kernels:
-                if k.name in self._constants:
-                    for v in k.writes():
-                        buffers.setdefault(v.buffer.name, self._empty(v.buffer))
-            self._bind_arena(buffers)
-            self._resident = buffers
-            self._static_inputs_flat = [buffers[v.buffer.name] for v in self.graph.inputs]
-        for dst, t in zip(self._static_inputs_flat, inputs):
-            dst.copy_(t.reshape(-1), non_blocking=True)
-        return self._resident
-
-    # -- execution --------------------------------------------------------------
-    def _build_plan(self, buffers: dict[str, torch.Tensor]) -> list:
-        plan: list = []
-        for k in self.schedule.kernels:
-            if k.name in self._constants:
-                bound = bind_extern(k, buffers, self._module)
-                run_bound_extern(bound)
-                plan.append(("const", bound))
-            elif isinstance(k, ExternKernel):
-                plan.append(("extern", bind_extern(k, buffers, self._module)))
-            else:
-                plan.append(("kernel", self._module.bind(k, buffers)))
-        compile_runs = getattr(self._module, "compile_runs", None)
-        self._runs = compile_runs(plan) if compile_runs is not None else plan
-        return plan
-
-    def _ensure_plan(self, buffers) -> None:
-        if self._plan is None:
-            self._plan = self._build_plan(buffers)
-
-    def run_kernels(self, buffers: dict[str, torch.Tensor]) -> None:
-        if self._plan is None or buffers is not self._resident:
-            for k in self.schedule.kernels:
-                self.run_one(k, buffers)
-        else:
-            run = self._module.run_bound
-            for kind, payload in self._runs:
-                if kind == "extern":
-                    run_bound_extern(payload)
-                elif kind == "kernel":
-                    run(payload)
-        fetch = getattr(self._module, "fetch_errors", None)
-        if fetch is not None:
-            fetch()
-
-    def run_one(self, k, buffers: dict[str, torch.Tensor]) -> None:
-        if isinstance(k, ExternKernel):
-            run_extern(k, buffers, self._module)
-        else:
-            self._module.launch(k, buffers)
-
-    def _run_eager(self, buffers: dict[str, torch.Tensor], plan) -> None:
-        for i, k in enumerate(self.schedule.kernels):
-            for b in plan.alloc_at.get(i, ()):
-                if b.name in self._live:
-                    buffers[b.name] = self._empty(b)
-            self.run_one(k, buffers)
-            for name in plan.free_at.get(i, ()):
-                buffers.pop(name, None)
-
-    def forward(self, *inputs: torch.Tensor):
-        plan = self.schedule.plan
-        if plan is not None and plan.mode == "eager":
-            buffers = self._bind_resident(inputs)
-            self._run_eager(buffers, plan)
-            return self._collect(buffers)
-        buffers = self._resident_buffers(inputs)
-        self._ensure_plan(buffers)
-        self.run_kernels(buffers)
-        return self._collect(buffers)
-
-    def _collect(self, buffers: dict[str, torch.Tensor]):
-        """Views of the output buffers; they alias storage the next call
-        overwrites (clone a result that must outlive the next call)."""
-        outs = [v.layout.as_torch(buffers[v.buffer.name]) for v in self.graph.outputs]
+    def _collect(self, table: dict[str, torch.Tensor]):
+        """Views of the outputs (aliasing storage the next call overwrites),
+        in the structure the module returned them."""
+        outs = [v.layout.as_torch(table[v.buffer.name]) for v in self.graph.outputs]
         spec = self.graph.meta.get("out_spec")
         if spec is not None:
             from torch.utils._pytree import tree_unflatten
@@ -235,11 +308,123 @@ class CompiledModel:
                 pass
         return outs[0] if len(outs) == 1 else tuple(outs)
 
+    # -- the plan ---------------------------------------------------------------
+    def _resolve(self, table: dict[str, torch.Tensor]) -> None:
+        """Bind every kernel once: ``[(kind, payload)]`` in schedule order,
+        with kind "const" (already run), "extern" or "kernel"."""
+        if self._plan is not None:
+            return
+        plan = []
+        for k in self.schedule.kernels:
+            if k.name in self._constants:
+                call = bind_extern(k, table, self._module)
+                call.run()
+                plan.append(("const", call))
+            elif isinstance(k, ExternKernel):
+                plan.append(("extern", bind_extern(k, table, self._module)))
+            else:
+                plan.append(("kernel", self._module.bind(k, table)))
+        self._plan = plan
+        group = getattr(self._module, "compile_runs", None)
+        self._runs = group(plan) if group is not None else plan
+
+    def run_one(self, k, table: dict[str, torch.Tensor]) -> None:
+        if isinstance(k, ExternKernel):
+            run_extern(k, table, self._module)
+        else:
+            self._module.launch(k, table)
+
+    def run_kernels(self, table: dict[str, torch.Tensor]) -> None:
+        """One pass of the schedule over ``table`` (through the resolved plan
+        when ``table`` is the resident one)."""
+        if self._plan is not None and table is self._buffers.table:
+            for kind, payload in self._runs:
+                if kind == "extern":
+                    payload.run()
+                elif kind == "kernel":
+                    self._module.run_bound(payload)
+        else:
+            for k in self.schedule.kernels:
+                self.run_one(k, table)
+        fetch = getattr(self._module, "fetch_errors", None)
+        if fetch is not None:
+            fetch()
+
+    def forward(self, *inputs: torch.Tensor):
+        """One uncaptured run."""
+        self._check_inputs(inputs)
+        plan = self.schedule.plan
+        if plan is not None and plan.mode == "eager":
+            table = self._buffers.per_call(inputs)
+            for i, k in enumerate(self.schedule.kernels):
+                for b in plan.alloc_at.get(i, ()):
+                    if b.name in self._buffers.live:
+                        table[b.name] = self._buffers.empty(b)
+                self.run_one(k, table)
+                for name in plan.free_at.get(i, ()):
+                    table.pop(name, None)
+            return self._collect(table)
+        table = self._buffers.resident(inputs)
+        self._resolve(table)
+        self.run_kernels(table)
+        return self._collect(table)
+
     def __call__(self, *inputs: torch.Tensor):
         self._raise_pending()
-        if self.cfg.cuda_graphs and self.device.type == "cuda":
-            return self._call_captured(inputs)
-        return self.forward(*inputs)
+        if not (self.cfg.cuda_graphs and self.device.type == "cuda"):
+            return self.forward(*inputs)
+        if not self._captured:
+            self._capture(inputs)
+        self._check_inputs(inputs)
+        for dst, src in zip(self._buffers.inputs, inputs):
+            dst.copy_(src.reshape(-1), non_blocking=True)
+        self._module.replay(torch.cuda.current_stream(self.device).cuda_stream)
+        return self._static_outputs
+
+    # -- capture ----------------------------------------------------------------
+    def _capture(self, inputs) -> None:
+        """Three warm-up runs on a side stream (modules loaded, library
+        workspaces allocated), then one run captured into the context's
+        hipGraph. Capture must allocate nothing: every library call writes a
+        pre-bound slice, and an allocation is reported with its culprits."""
+        self._check_inputs(inputs)
+        table = self._buffers.resident(inputs)
+        self._resolve(table)
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                self.run_kernels(table)
+            side.synchronize()
+            before = _alloc_count(self.device)
+            self._module.capture_begin(side.cuda_stream)
+            try:
+                self.run_kernels(table)
+            finally:
+                self._module.capture_end()
+            grew = _alloc_count(self.device) - before
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        if grew:
+            raise ExecutionError(f"{grew} device allocation(s) during graph capture would leave "
+                                 "the graph pointing at memory it does not own; allocating "
+                                 f"plan entries: {self._allocating_entries(side)}")
+        self._capture_stream = side
+        self._captured = True
+        self._static_outputs = self._collect(table)
+
+    def _allocating_entries(self, stream) -> list[str]:
+        culprits = []
+        with torch.cuda.stream(stream):
+            for kernel, (kind, payload) in zip(self.schedule.kernels, self._plan):
+                before = _alloc_count(self.device)
+                if kind == "extern":
+                    payload.run()
+                elif kind == "kernel":
+                    self._module.run_bound(payload)
+                if _alloc_count(self.device) != before:
+                    culprits.append(kernel.summary())
+        stream.synchronize()
+        return culprits
 
     # -- invalid inputs -------------------------------------------------------
     def _raise_pending(self) -> None:
@@ -265,93 +450,36 @@ class CompiledModel:
             torch.cuda.synchronize(self.device)
         self._raise_pending()
 
-    # -- graph replay -----------------------------------------------------------
-    def _call_captured(self, inputs):
-        if not self._captured:
-            self._capture(inputs)
-        else:
-            self._check_inputs(inputs)
-        for dst, src in zip(self._static_inputs, inputs):
-            dst.copy_(src.reshape(-1), non_blocking=True)
-        self._module.replay(torch.cuda.current_stream(self.device).cuda_stream)
-        return self._static_outputs
-
-    def _capture(self, inputs) -> None:
-        """Warm up three times on a side stream (kernels loaded, library
-        workspaces allocated), then capture one run into the context's
-        hipGraph. Capture must not allocate: every extern writes into a
-        pre-bound slice, and an allocation during capture is an error."""
-        buffers = self._resident_buffers(inputs)
-        self._ensure_plan(buffers)
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(side):
-            for _ in range(3):
-                self.run_kernels(buffers)
-            side.synchronize()
-            before = _alloc_count(self.device)
-            self._module.capture_begin(side.cuda_stream)
-            try:
-                self.run_kernels(buffers)
-            finally:
-                self._module.capture_end()
-            after = _alloc_count(self.device)
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        if after != before:
-            culprits = self._allocating_entries(side)
-            raise ExecutionError(f"{after - before} device allocation(s) happened during graph "
-                                 "capture; the captured graph would reference memory it does not "
-                                 f"own (allocating entries: {culprits})")
-        self._capture_stream = side
-        self._captured = True
-        self._static_inputs = [buffers[v.buffer.name] for v in self.graph.inputs]
-        self._static_outputs = self._collect(buffers)
-
-    def _allocating_entries(self, stream) -> list[str]:
-        """Plan entries that allocate device memory each time they run."""
-        found = []
-        with torch.cuda.stream(stream):
-            for kernel, (kind, payload) in zip(self.schedule.kernels, self._plan):
-                before = _alloc_count(self.device)
-                if kind == "extern":
-                    run_bound_extern(payload)
-                elif kind == "kernel":
-                    self._module.run_bound(payload)
-                if _alloc_count(self.device) != before:
-                    found.append(kernel.summary())
-        stream.synchronize()
-        return found
-
+    # -- profiling and introspection --------------------------------------------
     def profile_kernels(self, inputs, iters: int = 20) -> list[tuple]:
-        """(name, summary, ms) per kernel, each timed in place on the launch
-        stream with events, in schedule order."""
+        """``(name, summary, ms)`` per kernel in schedule order, each timed in
+        place on the launch stream: generated kernels by the runtime's
+        hipEvents, library calls by torch events."""
         if self.device.type != "cuda":
-            raise ExecutionError("kernel profiling needs a GPU device")
-        buffers = self._resident_buffers(inputs)
-        self._ensure_plan(buffers)
+            raise ExecutionError("profiling kernels needs the GPU")
+        table = self._buffers.resident(inputs)
+        self._resolve(table)
         for _ in range(3):
-            self.run_kernels(buffers)
+            self.run_kernels(table)
         torch.cuda.synchronize(self.device)
-        out = []
         stream = torch.cuda.current_stream(self.device)
+        rows = []
         for kernel, (kind, payload) in zip(self.schedule.kernels, self._plan):
             if kind == "kernel":
                 ms = self._module.time_bound(payload, iters, stream.cuda_stream)
             else:
                 for _ in range(3):
-                    run_bound_extern(payload)
-                start = torch.cuda.Event(enable_timing=True)
-                end = torch.cuda.Event(enable_timing=True)
+                    payload.run()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 start.record(stream)
                 for _ in range(iters):
-                    run_bound_extern(payload)
+                    payload.run()
                 end.record(stream)
                 end.synchronize()
                 ms = start.elapsed_time(end) / iters
-            out.append((kernel.name, kernel.summary(), ms))
-        return out
+            rows.append((kernel.name, kernel.summary(), ms))
+        return rows
 
-    # -- introspection ------------------------------------------------------------
     def source(self) -> str:
         """The generated module text (``mlc/runtime/executor.py:354-358``)."""
         return self._module.source
@@ -359,103 +487,6 @@ class CompiledModel:
     def source_path(self):
         return getattr(self._module, "path", None)
 
-    def __repr__(self) -> str:  # pragma: no cover
+    def __repr__(self) -> str:  # pragma: no cover - debug aid
         return (f"CompiledModel({self.graph.name}, {len(self.schedule)} kernels, "
                 f"backend={self.backend}, device={self.device})")
-
-
-def _alloc_count(device) -> int:
-    stats = torch.cuda.memory_stats(device)
-    return int(stats.get("allocation.all.allocated", 0))
-
-
-# ----------------------------------------------------------------------------
-# extern dispatch
-# ----------------------------------------------------------------------------
-
-def _materialise(a, buffers):
-    if isinstance(a, Value):
-        return a.layout.as_torch(buffers[a.buffer.name])
-    if isinstance(a, (list, tuple)):
-        return type(a)(_materialise(x, buffers) for x in a)
-    return a
-
-
-def bind_extern(k: ExternKernel, buffers: dict[str, torch.Tensor], module=None):
-    """Resolve an extern call against the fixed buffer table (never runs it).
-    A runner may claim the op with a native kernel (``bind_native_extern``)."""
-    node = k.node
-    native = getattr(module, "bind_native_extern", None)
-    if native is not None:
-        bound = native(k, buffers)
-        if bound is not None:
-            return ("native", module, bound)
-    target = node.meta.get("target")
-    if target is None:
-        raise ExecutionError(f"{node.op} has no dispatch target")
-    args = [_materialise(a, buffers) for a in node.args]
-    kwargs = {n: _materialise(v, buffers) for n, v in node.kwargs.items()}
-    variant = out_variant(node)
-    dest = None
-    if variant is not None:
-        out = node.outputs[0]
-        dest = out.layout.as_torch(buffers[out.buffer.name])
-    outs = [buffers[o.buffer.name] for o in node.outputs]
-    return ("torch", target, variant, args, kwargs, dest, outs)
-
-
-def run_bound_extern(bound) -> None:
-    if bound[0] == "native":
-        _, module, payload = bound
-        module.run_bound(payload)
-        return
-    _, target, variant, args, kwargs, dest, outs = bound
-    if variant is not None:
-        variant(*args, **kwargs, out=dest)
-        return
-    result = target(*args, **kwargs)
-    results = result if isinstance(result, (list, tuple)) else [result]
-    for buf, r in zip(outs, results):
-        buf.copy_(r.contiguous().reshape(-1))
-
-
-def out_variant(node):
-    """The op's ``.out`` overload when it takes exactly the default overload's
-    arguments plus ``out`` (decided from the schema, never by calling it)."""
-    if "out_variant" in node.meta:
-        return node.meta["out_variant"]
-    found = None
-    target = node.meta.get("target")
-    if (node.op.startswith("aten.") and len(node.outputs) == 1 and target is not None
-            and hasattr(target, "_schema")):
-        packet = getattr(torch.ops.aten, node.op.split(".")[1], None)
-        overload = getattr(packet, "out", None) if packet is not None else None
-        if overload is not None and _same_arguments(target, overload):
-            found = overload
-    node.meta["out_variant"] = found
-    return found
-
-
-def _same_arguments(default, out_overload) -> bool:
-    try:
-        want = [a.name for a in default._schema.arguments]
-        have = [a.name for a in out_overload._schema.arguments]
-    except AttributeError:
-        return False
-    return have[:len(want)] == want and have[len(want):] == ["out"]
-
-
-def run_extern(k: ExternKernel, buffers: dict[str, torch.Tensor], module=None) -> None:
-    """Dispatch one extern op through the flat buffers (unplanned path). An
-    ``.out`` overload that rejects the call is dropped for this node and the
-    op runs functionally, copied into its buffer."""
-    bound = bind_extern(k, buffers, module)
-    if bound[0] == "torch" and bound[2] is not None:
-        _, target, variant, args, kwargs, dest, outs = bound
-        try:
-            variant(*args, **kwargs, out=dest)
-            return
-        except (RuntimeError, TypeError):
-            k.node.meta["out_variant"] = None
-            bound = ("torch", target, None, args, kwargs, None, outs)
-    run_bound_extern(bound)

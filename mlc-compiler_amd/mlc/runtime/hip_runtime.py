@@ -220,8 +220,8 @@ class HipRuntime:
         def native_of(kind, payload):
             if kind == "kernel":
                 return payload if payload.grid else None
-            if kind == "extern" and payload[0] == "native" and payload[1] is self:
-                return payload[2]
+            if kind == "extern" and getattr(payload, "module", None) is self:
+                return payload.bound  # a library op this module claimed
             return None
 
         kernels = [b for b in (native_of(kind, p) for kind, p in plan) if b is not None]

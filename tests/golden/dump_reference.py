@@ -7,6 +7,10 @@ size, lower bound, unplanned total and every arena offset, plus -- for the
 toy models -- the reference's torch-backend outputs. Nothing else pins these:
 the published numbers only give kernel counts and arena totals.
 
+The models are this repository's own (``tests/models.py`` and
+``mlc-compiler_amd/mlc/bench/models.py``, which import torch only), loaded by
+file path and compiled by the reference compiler.
+
 Usage (from the repository root)::
 
     python tests/golden/dump_reference.py /root/reference tests/golden/reference_schedules.json
@@ -17,8 +21,20 @@ process so the reference's ``mlc`` package never meets this repository's.
 
 from __future__ import annotations
 
+import importlib.util
 import json
+import pathlib
 import sys
+
+REPO = pathlib.Path(__file__).resolve().parents[2]
+
+
+def _load(path: pathlib.Path, name: str):
+    spec = importlib.util.spec_from_file_location(name, path)
+    module = importlib.util.module_from_spec(spec)
+    sys.modules[name] = module  # dataclasses look their module up by name
+    spec.loader.exec_module(module)
+    return module
 
 
 def _describe(sched):
@@ -60,15 +76,16 @@ def _plan(sched):
 
 def main(ref_root: str, out_path: str) -> None:
     sys.path.insert(0, ref_root)
-    sys.path.insert(0, ref_root + "/tests")
     import torch
 
     import mlc
     from mlc.api import build_pipeline
-    from mlc.bench.models import build
     from mlc.config import Config
     from mlc.ir.capture import capture
-    from models import all_models
+
+    all_models = _load(REPO / "tests" / "models.py", "repo_toy_models").all_models
+    build = _load(REPO / "mlc-compiler_amd" / "mlc" / "bench" / "models.py",
+                  "repo_bench_models").build
 
     configs = {
         "no_fusion": Config(elementwise_fusion=False, recompute=False, reduction_fusion=False,

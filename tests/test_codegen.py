@@ -122,8 +122,8 @@ def test_launch_table_covers_every_generated_kernel(name, cfg):
 
 
 def test_generation_is_deterministic():
-    a = build_module(_sched("block"), FULL).source
-    b = build_module(_sched("block"), FULL).source
+    a = build_module(_sched("pre_norm_block"), FULL).source
+    b = build_module(_sched("pre_norm_block"), FULL).source
     assert a == b
 
 
@@ -132,7 +132,7 @@ def test_generate_module_returns_the_source_text():
     ``generate_module(schedule, cfg) -> str`` does
     (``mlc/codegen/triton_backend.py:261-287``); the launch table is
     ``build_module``'s."""
-    sched = _sched("block")
+    sched = _sched("pre_norm_block")
     src = generate_module(sched, FULL)
     assert isinstance(src, str)
     assert src == build_module(sched, FULL).source
@@ -175,15 +175,15 @@ def test_embedding_runs_as_a_native_template():
 
 
 def test_no_packed_fp32_by_hand_and_no_scalar_stores():
-    src = build_module(_sched("block"), FULL).source
+    src = build_module(_sched("pre_norm_block"), FULL).source
     text = src + native.TEMPLATES.joinpath("mlc_cdna4.h").read_text()
     assert not re.search(r"v_pk_(add|mul|fma)_f32", text)
     assert "-packed-fp32-ops" in native.HIP_FLAGS
     assert "asm" not in text
 
 
-@pytest.mark.parametrize("name,cfg", [("block", FULL), ("softmax", STREAMED),
-                                      ("masked", FULL), ("layernorm_scale", STREAMED)])
+@pytest.mark.parametrize("name,cfg", [("pre_norm_block", FULL), ("masked_softmax", STREAMED),
+                                      ("where_clamp_sum", FULL), ("norm_affine", STREAMED)])
 def test_module_cross_compiles_for_gfx950(name, cfg, tmp_path, monkeypatch):
     monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
     mod = build_module(_sched(name, cfg), cfg)

@@ -26,14 +26,14 @@ def _model(name):
 
 
 def test_wrong_input_shape_is_rejected():
-    _, model, args = _model("pointwise")
+    _, model, args = _model("two_input_chain")
     compiled = compile_reference(model, args, FULL)
     with pytest.raises(ExecutionError, match="compiled for"):
         compiled(torch.randn(5, 16), torch.randn(5, 16))
 
 
 def test_outputs_alias_static_storage():
-    _, model, args = _model("residual_chain")
+    _, model, args = _model("shared_producer")
     compiled = compile_reference(model, args, FULL)
     first = compiled(*args)
     kept = first.clone()
@@ -43,7 +43,7 @@ def test_outputs_alias_static_storage():
 
 
 def test_inputs_are_copied_not_aliased():
-    _, model, args = _model("pointwise")
+    _, model, args = _model("two_input_chain")
     compiled = compile_reference(model, args, FULL)
     x = args[0].clone()
     out = compiled(x, args[1]).clone()
@@ -53,7 +53,7 @@ def test_inputs_are_copied_not_aliased():
 
 
 def test_arena_offsets_bind_buffers():
-    _, model, args = _model("block")
+    _, model, args = _model("pre_norm_block")
     compiled = compile_reference(model, args, FULL)
     compiled(*args)
     arena = compiled._arena
@@ -68,7 +68,7 @@ def test_arena_offsets_bind_buffers():
 
 def test_product_refuses_the_cpu():
     """No silent CPU fallback: mlc.compile on a CPU model raises."""
-    _, model, args = _model("pointwise")
+    _, model, args = _model("two_input_chain")
     with pytest.raises(ExecutionError, match="ROCm GPU"):
         mlc.compile(model, args, FULL)
     with pytest.raises(ExecutionError):
@@ -80,7 +80,7 @@ def test_hip_runtime_refuses_a_cpu_device():
     from mlc.runtime.hip_runtime import HipRuntime
     from mlc.runtime.native import NativeError
 
-    _, model, args = _model("pointwise")
+    _, model, args = _model("two_input_chain")
     from mlc.api import build_pipeline
     from mlc.ir.capture import capture
 

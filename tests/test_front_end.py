@@ -143,7 +143,7 @@ def test_schedule_invariants(name, cname):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("name", ["pointwise", "mlp", "softmax", "layernorm_scale", "block"])
+@pytest.mark.parametrize("name", ["two_input_chain", "feed_forward", "masked_softmax", "norm_affine", "pre_norm_block"])
 def test_narrow_float_models(name, dtype):
     """fp16/bf16 storage through the kernel IR (fp32 math inside kernels):
     within 1e-2/5e-2 of eager in the same dtype and 2e-2/5e-2 of eager fp32
@@ -164,7 +164,7 @@ def test_binding_an_extern_never_runs_it():
     """Resolving an extern against the buffer table leaves its outputs
     untouched; only running the bound call writes them (reference
     ``tests/test_bench_reporting.py:77-111``)."""
-    _, model, args = next(t for t in all_models() if t[0] == "mlp")
+    _, model, args = next(t for t in all_models() if t[0] == "feed_forward")
     graph = capture(model, args)
     sched = build_pipeline(graph, Config(memory_planning=False, cuda_graphs=False))
     externs = [k for k in sched.kernels if isinstance(k, ExternKernel)]

@@ -184,12 +184,12 @@ def _reductions(sched):
 
 
 def test_online_softmax_detection_and_passes():
-    _, model, args = _model("softmax")
+    _, model, args = _model("masked_softmax")
     k = _reductions(build_pipeline(capture(model, args), STREAMED))[0]
     assert detect_online_softmax(k) is not None
     passes = plan_passes(k)
     assert len(passes) == 2 and passes[0].online_softmax is not None
-    _, model, args = _model("layernorm_scale")
+    _, model, args = _model("norm_affine")
     ln = _reductions(build_pipeline(capture(model, args), STREAMED))[0]
     assert detect_online_softmax(ln) is None
     vector, scalars = varies_by_column(ln), {b.name for b in scalar_binds(ln)}
@@ -202,7 +202,7 @@ def test_online_softmax_detection_and_passes():
                                       ("rsqrt", torch.sqrt)])
 def test_planted_oracle_mistake_is_caught(monkeypatch, fn, wrong):
     monkeypatch.setitem(tr.TORCH_FN, fn, wrong)
-    _, model, args = _model("block")
+    _, model, args = _model("pre_norm_block")
     with torch.no_grad():
         want = model(*args)
     got = compile_reference(model, args, FULL)(*args)
