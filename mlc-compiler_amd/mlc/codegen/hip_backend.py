@@ -108,12 +108,39 @@ class Renderer:
     """Renders scalar expressions to C++ with their register types.
 
     ``operand(slot)`` and ``temp(name)`` give the C++ expression (and type)
-    that reads an input or a temporary at the current element.
+    that reads an input or a temporary at the current element. ``half_slots``
+    are the inputs stored as fp16 and ``defs`` the temporaries' defining
+    expressions: with them, fp32 add/sub/mul with an operand just converted
+    from fp16 render as the equal fma against an opaque constant (the
+    hardware's mixed-precision fma reads the fp16 half directly), and
+    ``X * 2^k + y`` with an fp16 ``X`` becomes one fma (``X * 2^k`` is exact
+    for every fp16 X when |k| <= 100, so the fma rounds once where the two
+    operations would round once too).
     """
 
-    def __init__(self, operand, temp) -> None:
+    def __init__(self, operand, temp, half_slots=frozenset(), defs=None, to_fp16=frozenset()) -> None:
         self.operand = operand
         self.temp = temp
+        self.half_slots = frozenset(half_slots)
+        self.defs = defs if defs is not None else {}
+        #: temporaries whose every use rounds them to fp16
+        self.to_fp16 = frozenset(to_fp16)
+        self._plain = False
+
+    def bind(self, name: str, e: Expr) -> tuple[str, str]:
+        """Render the defining expression of temporary ``name``. An add, sub
+        or mul of two fp16 values whose result is only rounded to fp16 stays
+        the plain operation: the compiler evaluates that in fp16 directly
+        (exact, since fp32 holds more than twice fp16's precision) with packed
+        half instructions, two elements per instruction."""
+        return self.store(e, name in self.to_fp16)
+
+    def store(self, e: Expr, to_fp16: bool) -> tuple[str, str]:
+        """Render ``e`` for a value that is only rounded to fp16 when ``to_fp16``."""
+        if (to_fp16 and isinstance(e, Call) and e.fn in ("add", "sub", "mul")
+                and all(self.is_half(a) for a in e.args)):
+            self._plain = True
+        return self(e)
 
     def __call__(self, e: Expr) -> tuple[str, str]:
         if isinstance(e, Load):
@@ -129,6 +156,65 @@ class Renderer:
             return self.call(e)
         raise TypeError(f"cannot emit {type(e).__name__}")
 
+    def is_half(self, e: Expr, depth: int = 0) -> bool:
+        """Whether ``e`` is an fp32 register holding a value converted from
+        fp16: an fp16 input, a rounding to fp16, or a temporary of either."""
+        if isinstance(e, Load):
+            return e.slot in self.half_slots
+        if isinstance(e, Cast):
+            return e.dtype == torch.float16 or (e.dtype == torch.float32 and self.is_half(e.x, depth))
+        if isinstance(e, Ref) and depth < 8:
+            d = self.defs.get(e.name)
+            return d is not None and self.is_half(d, depth + 1)
+        return False
+
+    def exact_scale(self, e: Expr):
+        """(X, c) when ``e`` is ``X * c`` or ``X / (1/c)`` with an fp16 ``X``
+        and ``c = +-2^k``, |k| <= 100, directly or through one temporary."""
+        if isinstance(e, Ref):
+            e = self.defs.get(e.name, e)
+        if not (isinstance(e, Call) and e.fn in ("mul", "div")):
+            return None
+        x, c = e.args
+        if e.fn == "mul" and isinstance(x, Const):
+            x, c = c, x
+        if not isinstance(c, Const) or not self.is_half(x):
+            return None
+        fast = _const_divisor(c)
+        if fast is None or not fast[2]:
+            return None
+        v = fast[0] if e.fn == "mul" else fast[1]
+        if not (2.0 ** -100 <= abs(v) <= 2.0 ** 100):
+            return None
+        return x, v
+
+    def mixed(self, e: Call, codes: list[str]) -> str | None:
+        """The fma form of an fp32 add/sub/mul described above, or None."""
+        x, y = e.args
+        if e.fn in ("add", "sub"):
+            sign = 1.0 if e.fn == "add" else -1.0
+            sx = self.exact_scale(x)
+            if sx is not None:  # X*c + y  or  X*c - y
+                other = codes[1] if e.fn == "add" else f"(-{codes[1]})"
+                return f"__builtin_fmaf({self(sx[0])[0]}, {float_literal(sx[1])}, {other})"
+            sy = self.exact_scale(y)
+            if sy is not None:  # x + Y*c  or  x - Y*c
+                return f"__builtin_fmaf({self(sy[0])[0]}, {float_literal(sign * sy[1])}, {codes[0]})"
+            if e.fn == "sub":
+                if self.is_half(x) or self.is_half(y):
+                    return f"__builtin_fmaf({codes[1]}, mlc::neg_one_(), {codes[0]})"
+                return None
+            if self.is_half(x):
+                return f"__builtin_fmaf({codes[0]}, mlc::one_(), {codes[1]})"
+            if self.is_half(y):
+                return f"__builtin_fmaf({codes[1]}, mlc::one_(), {codes[0]})"
+            return None
+        if self.is_half(x):
+            return f"__builtin_fmaf({codes[0]}, {codes[1]}, mlc::neg_zero_())"
+        if self.is_half(y):
+            return f"__builtin_fmaf({codes[1]}, {codes[0]}, mlc::neg_zero_())"
+        return None
+
     @staticmethod
     def const(e: Const) -> tuple[str, str]:
         v, dt = e.value, e.dtype
@@ -143,6 +229,7 @@ class Renderer:
         return float_literal(float(v)), "float"
 
     def call(self, e: Call) -> tuple[str, str]:
+        plain, self._plain = self._plain, False
         args = [self(a) for a in e.args]
         codes = [c for c, _ in args]
         types = [t for _, t in args]
@@ -150,6 +237,10 @@ class Renderer:
         fn = e.fn
         a = codes[0]
         if fn in ("add", "sub", "mul"):
+            if types[0] == "float" and types[1] == "float" and not plain:
+                m = self.mixed(e, codes)
+                if m is not None:
+                    return m, "float"
             op = {"add": "+", "sub": "-", "mul": "*"}[fn]
             t = "int64_t" if top == "bool" else top
             return f"({a} {op} {codes[1]})", t
@@ -161,6 +252,8 @@ class Renderer:
                 if fast is not None:
                     c, y, exact_mul = fast
                     if exact_mul:
+                        if self.is_half(e.args[0]):
+                            return f"__builtin_fmaf({a}, {float_literal(y)}, mlc::neg_zero_())", "float"
                         return f"({a} * {float_literal(y)})", "float"
                     return f"mlc::div_rcp({a}, {float_literal(c)}, {float_literal(y)})", "float"
             return f"({a} / {codes[1]})", top
@@ -197,6 +290,70 @@ class Renderer:
             arg = a if types[0] in ("float", "double", "int64_t") else f"(float)({a})"
             return f"mlc::{fn}_({arg})", t
         raise KeyError(f"no HIP form for scalar function {fn!r}")
+
+
+def half_inputs(k) -> frozenset[int]:
+    """Input slots stored as fp16 (read into fp32 registers by conversion)."""
+    return frozenset(i for i, a in enumerate(k.inputs) if a.dtype == torch.float16)
+
+
+def bind_defs(k: ReductionKernel) -> dict[str, Expr]:
+    return {s.name: s.expr for s in k.steps if isinstance(s, Bind)}
+
+
+HALF_STORAGE = (torch.float16, torch.bfloat16)
+
+
+def rounded_only(name: str, exprs, stores, dtypes=HALF_STORAGE) -> bool:
+    """Whether temporary ``name`` reaches nothing but a rounding to one of
+    ``dtypes``: every use in ``exprs`` is a cast of it to such a type, and
+    every store of it (``stores``: (expression, storage dtype) pairs) is into
+    such a type. Its fp32 value is then never seen except through that
+    rounding."""
+    target = Ref(name)
+
+    def bare_use(e) -> bool:
+        if e == target:
+            return True
+        if isinstance(e, Cast):
+            if e.x == target and e.dtype in dtypes:
+                return False
+            return bare_use(e.x)
+        if isinstance(e, Call):
+            return any(bare_use(a) for a in e.args)
+        return False
+
+    if any(bare_use(e) for e in exprs):
+        return False
+    for e, dt in stores:
+        if e == target:
+            if dt not in dtypes:
+                return False
+        elif bare_use(e):
+            return False
+    return True
+
+
+def _uses(k):
+    """(expressions, (stored expression, storage dtype) pairs) of a kernel."""
+    if isinstance(k, ReductionKernel):
+        exprs = [s.expr for s in k.steps]
+    else:
+        exprs = [e for _, e in k.body]
+    return exprs, [(k.out_expr[a.value.name], a.dtype) for a in k.outputs]
+
+
+def storage_rounded(k: ReductionKernel, name: str) -> bool:
+    """``rounded_only`` for a temporary of ``k``, to fp16 or bf16."""
+    return rounded_only(name, *_uses(k))
+
+
+def fp16_rounded(k) -> frozenset[str]:
+    """Temporaries of ``k`` that only reach a rounding to fp16."""
+    exprs, stores = _uses(k)
+    names = [s.name for s in k.steps if isinstance(s, Bind)] if isinstance(k, ReductionKernel) \
+        else [n for n, _ in k.body]
+    return frozenset(n for n in names if rounded_only(n, exprs, stores, (torch.float16,)))
 
 
 def _fp32(v: float) -> float:
@@ -392,11 +549,15 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
     L.append(f"  const {it} e0 = (base + ({it})u * {B}) * V;")
     L.append("  if (e0 >= N) break;")
 
+    half_slots = half_inputs(k)
+    defs = dict(k.body)
+    to_fp16 = fp16_rounded(k)
+
     def body_lines(ref_in, indent: str) -> list[str]:
         lines = []
-        r = Renderer(ref_in, lambda n: (n, temp_types[n]))
+        r = Renderer(ref_in, lambda n: (n, temp_types[n]), half_slots, defs, to_fp16)
         for name, expr in k.body:
-            code, t = r(expr)
+            code, t = r.bind(name, expr)
             temp_types[name] = t
             lines.append(f"{indent}const {t} {name} = {code};")
         return lines, r
@@ -431,7 +592,7 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
     blines, r = body_lines(ref_vec, "      ")
     vec += blines
     for i, a in enumerate(k.outputs):
-        code, _ = r(k.out_expr[a.value.name])
+        code, _ = r.store(k.out_expr[a.value.name], a.dtype == torch.float16)
         vec.append(f"      o{i}[j] = {code};")
     vec.append("    }")
     for i, (a, acc) in enumerate(zip(k.outputs, out_access)):
@@ -457,7 +618,7 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
         blines, r = body_lines(lambda s: (f"s{s}", in_types[s]), "      ")
         L += blines
         for i, a in enumerate(k.outputs):
-            code, _ = r(k.out_expr[a.value.name])
+            code, _ = r.store(k.out_expr[a.value.name], a.dtype == torch.float16)
             L.append(f"      mlc::st(out{i} + {offset(a, 'e')}, {code});")
         L.append("    }")
         L.append("  }")
@@ -827,8 +988,9 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
         return name, temp_types[name]
 
     nonpos = nonpositive_args(k)
-    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos)
-    scal_r = Renderer(ref_scalar, temp_scalar)
+    half_slots, defs, to_fp16 = half_inputs(k), bind_defs(k), fp16_rounded(k)
+    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos, half_slots, defs, to_fp16)
+    scal_r = Renderer(ref_scalar, temp_scalar, half_slots, defs, to_fp16)
     rcp_for = _reciprocal_divisors(k, vector)
 
     def elem_loop(target: str, code: str) -> list[str]:
@@ -838,22 +1000,24 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
     for s in k.steps:
         if isinstance(s, Bind):
             if s.name in vector:
-                code, t = elem_r(s.expr)
+                code, t = elem_r.bind(s.name, s.expr)
                 temp_types[s.name] = t
                 L.append(f"  {t} {s.name}[K][V];")
                 sd = _scalar_division(s.expr, rcp_for)
-                if sd is not None and t == "float":
+                if sd is not None and t == "float" and softmax_sum(k, sd[1], nonpos):
                     num, d = elem_r(sd[0])[0], sd[1]
-                    div = "div_rcp_finite" if _bounded_exp(sd[0], k, nonpos) else "div_rcp"
+                    L += elem_loop(s.name, _row_division(k, s.name, sd[0], num, d, nonpos))
+                elif sd is not None and t == "float":
+                    num, d = elem_r(sd[0])[0], sd[1]
                     L.append(f"  if (__all(ok_{d})) {{")
-                    L += elem_loop(s.name, f"mlc::{div}({num}, {d}, rcp_{d})")
+                    L += elem_loop(s.name, _row_division(k, s.name, sd[0], num, d, nonpos))
                     L.append("  } else {")
                     L += elem_loop(s.name, code)
                     L.append("  }")
                 else:
                     L += elem_loop(s.name, code)
             else:
-                code, t = scal_r(s.expr)
+                code, t = scal_r.bind(s.name, s.expr)
                 temp_types[s.name] = t
                 L.append(f"  const {t} {s.name} = {code};")
                 L += _reciprocal_lines(s.name, rcp_for)
@@ -908,10 +1072,11 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
         if not exact:
             L.append("      if (!valid[p]) continue;")
         L.append(f"      const {it} c0 = (({it})p * G + lane) * V;")
+        half_out = a.dtype == torch.float16
         if _expr_varies(e, col_slots, vector):
-            code, _ = elem_r(e)
+            code, _ = elem_r.store(e, half_out)
         else:
-            code, _ = scal_r(e)
+            code, _ = scal_r.store(e, half_out)
         L.append(f"      {ot} o[V];")
         L.append("#pragma unroll")
         L.append(f"      for (int j = 0; j < V; ++j) o[j] = {code};")
@@ -928,7 +1093,7 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
     if row_store:
         L.append("  if (lane == 0) {")
         for i, a in row_store:
-            code, _ = scal_r(k.out_expr[a.value.name])
+            code, _ = scal_r.store(k.out_expr[a.value.name], a.dtype == torch.float16)
             L.append(f"    mlc::st(out{i} + {offs.row(a)}, {code});")
         L.append("  }")
     L.append("}")
@@ -979,11 +1144,40 @@ def _bounded_exp(e: Expr, k: ReductionKernel, nonpos: set) -> bool:
     return isinstance(e, Call) and e.fn == "exp" and e.args[0] in nonpos
 
 
+def softmax_sum(k: ReductionKernel, name: str, nonpos) -> bool:
+    """Whether ``name`` is a row sum of ``exp(x - rowmax(x))`` (``nonpos``
+    holds those arguments). The row's maximum element contributes exp(0) = 1
+    and no term is negative, so the sum lies in [1, row length] or is NaN:
+    always in the range where the hoisted reciprocal is exact enough, so its
+    divisions need no range guard (a NaN sum gives NaN either way)."""
+    step = next((s for s in k.steps if s.name == name), None)
+    return (isinstance(step, Reduce) and step.kind == "sum"
+            and _bounded_exp(step.expr, k, nonpos))
+
+
+def _row_division(k: ReductionKernel, name: str, num_expr: Expr, num: str, d: str, nonpos) -> str:
+    """Per-element ``num / d`` for a row-uniform divisor with ``rcp_d`` =
+    RN(1/d) hoisted and d in the normal range (the caller's guard).
+
+    A quotient that only reaches a rounding to fp16/bf16 is ``num * rcp_d``:
+    at most 1.5 fp32 ulp from the quotient, 2^12 times below the half ulp of
+    fp16 that the rounding then adds. The correctly rounded quotient and this
+    product round to different fp16 values only when they straddle an fp16
+    rounding boundary, and then by one fp16 ulp. Any other quotient is
+    correctly rounded (``mlc::div_rcp``; ``div_rcp_finite`` when the numerator
+    is a softmax's exp, never infinite)."""
+    if storage_rounded(k, name):
+        return f"({num} * rcp_{d})"
+    div = "div_rcp_finite" if _bounded_exp(num_expr, k, nonpos) else "div_rcp"
+    return f"mlc::{div}({num}, {d}, rcp_{d})"
+
+
 class _NonPosExpRenderer(Renderer):
     """``exp`` of an argument known to be at most 0 as ``mlc::exp_nonpos``."""
 
-    def __init__(self, operand, temp, nonpos: set) -> None:
-        super().__init__(operand, temp)
+    def __init__(self, operand, temp, nonpos: set, half_slots=frozenset(), defs=None,
+                 to_fp16=frozenset()) -> None:
+        super().__init__(operand, temp, half_slots, defs, to_fp16)
         self.nonpos = nonpos
 
     def call(self, e: Call) -> tuple[str, str]:
@@ -1089,8 +1283,9 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
         return name, temp_types[name]
 
     nonpos = nonpositive_args(k)
-    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos)
-    scal_r = Renderer(lambda s: (f"v{s}", in_types[s]), temp_scalar)
+    half_slots, defs, to_fp16 = half_inputs(k), bind_defs(k), fp16_rounded(k)
+    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos, half_slots, defs, to_fp16)
+    scal_r = Renderer(lambda s: (f"v{s}", in_types[s]), temp_scalar, half_slots, defs, to_fp16)
     rcp_for = _reciprocal_divisors(k, vector)
 
     def slots_for(p) -> list[int]:
@@ -1128,15 +1323,20 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
                 out.append("#pragma unroll")
                 out.append(f"    for (int j = 0; j < V; ++j) v{i}[j] = mlc::ld(in{i} + {offs.row(a)} + {offs.col(a, '(c0 + (' + it + ')j)')});")
         for b in p.binds:
-            code, t = elem_r(b.expr)
+            code, t = elem_r.bind(b.name, b.expr)
             out.append(f"    {t} {b.name}[V];")
             sd = _scalar_division(b.expr, rcp_for)
-            if sd is not None and t == "float":
+            if sd is not None and t == "float" and softmax_sum(k, sd[1], nonpos):
                 num, d = elem_r(sd[0])[0], sd[1]
-                div = "div_rcp_finite" if _bounded_exp(sd[0], k, nonpos) else "div_rcp"
+                out.append("#pragma unroll")
+                out.append(f"    for (int j = 0; j < V; ++j) {b.name}[j] = "
+                           f"{_row_division(k, b.name, sd[0], num, d, nonpos)};")
+            elif sd is not None and t == "float":
+                num, d = elem_r(sd[0])[0], sd[1]
                 out.append(f"    if (__all(ok_{d})) {{")
                 out.append("#pragma unroll")
-                out.append(f"      for (int j = 0; j < V; ++j) {b.name}[j] = mlc::{div}({num}, {d}, rcp_{d});")
+                out.append(f"      for (int j = 0; j < V; ++j) {b.name}[j] = "
+                           f"{_row_division(k, b.name, sd[0], num, d, nonpos)};")
                 out.append("    } else {")
                 out.append("#pragma unroll")
                 out.append(f"      for (int j = 0; j < V; ++j) {b.name}[j] = {code};")
@@ -1169,7 +1369,7 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             acc = _row_col_access(k, a, V)
             ot = compute_type_of_out(k, a)
             e = k.out_expr[nm]
-            code, _ = (elem_r(e) if _expr_varies(e, col_slots, vector) else scal_r(e))
+            code, _ = (elem_r if _expr_varies(e, col_slots, vector) else scal_r).store(e, a.dtype == torch.float16)
             out.append(f"    {{ {ot} o[V];")
             out.append("#pragma unroll")
             out.append(f"      for (int j = 0; j < V; ++j) o[j] = {code};")
@@ -1203,10 +1403,9 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             if id(p) in emitted:
                 continue
             emitted.add(id(p))
-            L.append("  {" if False else "")
             L += emit_pass(p)
         elif s.name in scalars:
-            code, t = scal_r(s.expr)
+            code, t = scal_r.bind(s.name, s.expr)
             L.append(f"  const {t} {s.name} = {code};")
             L += _reciprocal_lines(s.name, rcp_for)
     for p in passes:
@@ -1216,7 +1415,7 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
     if row_store:
         L.append("  if (lane == 0) {")
         for i, a in row_store:
-            code, _ = scal_r(k.out_expr[a.value.name])
+            code, _ = scal_r.store(k.out_expr[a.value.name], a.dtype == torch.float16)
             L.append(f"    mlc::st(out{i} + {offs.row(a)}, {code});")
         L.append("  }")
     L.append("}")

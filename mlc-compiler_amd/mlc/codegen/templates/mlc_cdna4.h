@@ -12,7 +12,10 @@
 //    per-wave partials through LDS in a fixed order;
 //  * scalar math helpers with torch semantics (NaN-propagating max/min,
 //    correctly rounded division, integer true division); transcendentals
-//    are ROCm's device math library.
+//    are ROCm's device math library, except erf and a softmax's exp of a
+//    non-positive argument, which are evaluated here;
+//  * mixed-precision forms of add, sub and mul (an fma against an opaque
+//    constant) that read fp16 operands without a separate conversion.
 //
 // No MFMA: every kernel generated here is HBM-bandwidth bound.
 #pragma once
@@ -151,17 +154,24 @@ __device__ __forceinline__ float exp_(float x) { return expf(x); }
 __device__ __forceinline__ float exp_fast(float x) {
   return __builtin_amdgcn_exp2f(x * 0x1.715476p+0f);
 }
-// exp(x) for x <= 0, -inf or NaN: a softmax's exp(x - rowmax(x)). With
-// x log2 e = n + f (n = rint, so |f| <= 1/2), f is formed with one rounding
-// from the exact product (fma) plus the low word of log2 e, 2^f comes from
-// v_exp_f32 and 2^n from ldexp (Cody and Waite's reduction). There is no
-// overflow to guard: x is at most 0, clamped below at -104 where exp is 0 in
-// fp32 (the NaN-propagating maximum keeps NaN, whose exponent is taken as 0).
+// exp(x) for x <= 0, -inf or NaN: a softmax's exp(x - rowmax(x)).
+// h = RN(x log2 e) goes to v_exp_f32 whole, and the rounding of h is put back
+// by one correction: with r = x - h ln2 (formed by two fmas against ln2 split
+// into an fp32 head and tail, so r carries no rounding error that matters;
+// |r| <= 8e-6 over the clamped range), exp(x) = 2^h e^r = 2^h (1 + r) up to
+// r^2/2 < 4e-11 relative. Error: v_exp_f32's (0.8 ulp measured) plus the
+// final fma's half ulp. v_exp_f32 flushes results below 2^-126 to zero, so
+// exp(x) < 2^-126 (x < -87.34) comes out as 0, an absolute error below
+// 1.2e-38. No overflow path: x is at most 0. The clamp at -104 (exp is 0 in
+// fp32 below it) keeps r finite for x = -inf; the NaN-propagating maximum
+// keeps NaN.
 __device__ __forceinline__ float exp_nonpos(float x) {
   x = __builtin_elementwise_maximum(x, -104.0f);
-  const float n = __builtin_rintf(x * 0x1.715476p+0f);
-  const float f = __builtin_fmaf(x, 0x1.4ae0c0p-26f, __builtin_fmaf(x, 0x1.715476p+0f, -n));
-  return __builtin_ldexpf(__builtin_amdgcn_exp2f(f), (int)__builtin_fminf(n, 0.0f));
+  const float h = x * 0x1.715476p+0f;
+  float r = __builtin_fmaf(-h, 0x1.62e430p-1f, x);
+  r = __builtin_fmaf(-h, -0x1.05c610p-29f, r);
+  const float e = __builtin_amdgcn_exp2f(h);
+  return __builtin_fmaf(e, r, e);
 }
 __device__ __forceinline__ double exp_(double x) { return exp(x); }
 // erf in fp32 from two polynomials fitted for this build (weighted least
@@ -274,6 +284,19 @@ __device__ __forceinline__ float div_rcp_finite(float x, float d, float y) {
   const float q = x * y;
   return __builtin_fmaf(__builtin_fmaf(-q, d, x), y, q);
 }
+// Constants hidden from the optimiser. fma(a, 1, b), fma(b, -1, a) and
+// fma(a, b, -0) are bit for bit a + b, a - b and a * b (one rounding of an
+// exact value, the same signed zeros), but the compiler folds them back into
+// the plain operation when it can see the constant. Kept opaque, the fma of a
+// value just converted from fp16 is selected as v_fma_mix_f32, which reads the
+// fp16 half directly and saves the v_cvt_f32_f16.
+__device__ __forceinline__ float opaque_(float v) {
+  asm("" : "+s"(v));
+  return v;
+}
+__device__ __forceinline__ float one_() { return opaque_(1.0f); }
+__device__ __forceinline__ float neg_one_() { return opaque_(-1.0f); }
+__device__ __forceinline__ float neg_zero_() { return opaque_(-0.0f); }
 // whether div_rcp is exact for every x with this divisor
 __device__ __forceinline__ bool rcp_ok(float d) {
   const float a = __builtin_fabsf(d);

@@ -179,7 +179,11 @@ def test_no_packed_fp32_by_hand_and_no_scalar_stores():
     text = src + native.TEMPLATES.joinpath("mlc_cdna4.h").read_text()
     assert not re.search(r"v_pk_(add|mul|fma)_f32", text)
     assert "-packed-fp32-ops" in native.HIP_FLAGS
-    assert "asm" not in text
+    # the one inline asm is an empty template that only hides a constant in
+    # an SGPR from the optimiser: it emits no instruction
+    opaque = 'asm("" : "+s"(v));'
+    assert text.count(opaque) == 1
+    assert "asm" not in text.replace(opaque, "")
 
 
 @pytest.mark.parametrize("name,cfg", [("pre_norm_block", FULL), ("masked_softmax", STREAMED),
@@ -225,3 +229,83 @@ def test_softmax_exp_has_no_overflow_path():
     body = src[src.index('extern "C"'):]
     assert "mlc::exp_nonpos(" in body and "mlc::div_rcp_finite(" in body
     assert "mlc::exp_(" in body
+
+
+def _body(model, *args):
+    cfg = Config(cuda_graphs=False)
+    src = build_module(build_pipeline(capture(model, args), cfg), cfg).source
+    return src[src.index('extern "C"'):]
+
+
+class _ScaledMaskedSoftmax(torch.nn.Module):
+    def forward(self, s, m):
+        return (s / 8.0 + m).softmax(dim=-1)
+
+
+def test_softmax_division_by_a_row_sum():
+    """A row sum of ``exp(x - rowmax(x))`` lies in [1, row length] (or is
+    NaN), so the division by it needs no range guard. Rounded to fp16 the
+    quotient is the product with the row reciprocal; kept in fp32 it stays
+    correctly rounded (``div_rcp_finite``)."""
+    s, m = torch.randn(4, 2, 16, 128), torch.zeros(4, 1, 1, 128)
+    b16 = _body(_ScaledMaskedSoftmax(), s.half(), m.half())
+    assert "* rcp_" in b16 and "div_rcp" not in b16 and "__all(ok_" not in b16
+    b32 = _body(_ScaledMaskedSoftmax(), s, m)
+    assert "mlc::div_rcp_finite(" in b32 and "__all(ok_" not in b32
+
+
+def test_other_row_divisions_keep_the_range_guard():
+    """A division by a row statistic that is not a softmax sum (here a sum of
+    squares, which can be 0 or huge) keeps the guarded fast path and the IEEE
+    fallback, even when its quotient is rounded to fp16."""
+    class Norm(torch.nn.Module):
+        def forward(self, x):
+            return x / (x * x).sum(dim=-1, keepdim=True)
+
+    body = _body(Norm(), torch.randn(8, 256).half())
+    assert "__all(ok_" in body and "* rcp_" in body
+
+
+def test_fp16_scale_and_add_is_one_fma():
+    """``s / 8 + m`` with fp16 ``s``: ``s * 2^-3`` is exact, so the pair is
+    one fma reading both fp16 operands (no separate conversion)."""
+    body = _body(_ScaledMaskedSoftmax(), torch.randn(4, 2, 16, 128).half(),
+                 torch.zeros(4, 1, 1, 128).half())
+    assert re.search(r"__builtin_fmaf\(v0\[p\]\[j\], 0x1\.0+p-3f, v1\[p\]\[j\]\)", body)
+    # an inexact scale is not contracted
+    class Inexact(torch.nn.Module):
+        def forward(self, s, m):
+            return (s * 0.3 + m).softmax(dim=-1)
+
+    body = _body(Inexact(), torch.randn(4, 128).half(), torch.randn(4, 128).half())
+    assert not re.search(r"__builtin_fmaf\(v0\[p\]\[j\], 0x1\.3[0-9a-f]+p-2f, v1", body)
+    assert re.search(r"__builtin_fmaf\(v0\[p\]\[j\], 0x1\.3[0-9a-f]+p-2f, mlc::neg_zero_\(\)\)", body)
+
+
+def test_mixed_precision_forms():
+    """fp32 arithmetic on fp16 operands renders as the equal fma against an
+    opaque constant, except an add of two fp16 values stored straight back to
+    fp16, which the compiler evaluates in packed fp16 itself."""
+    class BiasAdd(torch.nn.Module):
+        def forward(self, x, b):
+            return x + b
+
+    body = _body(BiasAdd(), torch.randn(64, 256).half(), torch.randn(256).half())
+    assert "(v0[j] + v1[j])" in body and "one_()" not in body
+
+    class AddThenNorm(torch.nn.Module):
+        def forward(self, x, r):
+            return torch.nn.functional.layer_norm(x + r, (256,))
+
+    body = _body(AddThenNorm(), torch.randn(64, 256).half(), torch.randn(64, 256).half())
+    assert "__builtin_fmaf(v0[p][j], mlc::one_(), v1[p][j])" in body
+
+    class SubMul(torch.nn.Module):
+        def forward(self, x, y):
+            return (x.float() - y.float()) * x.float()
+
+    body = _body(SubMul(), torch.randn(64, 256).half(), torch.randn(64, 256).half())
+    assert "mlc::neg_one_()" in body and "mlc::neg_zero_()" in body
+    # fp32 operands keep the plain operators
+    body = _body(SubMul(), torch.randn(64, 256), torch.randn(64, 256))
+    assert "one_()" not in body and "neg_zero_()" not in body
