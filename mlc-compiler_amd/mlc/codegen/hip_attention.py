@@ -41,11 +41,12 @@ from __future__ import annotations
 
 import torch
 
+from ..ir.scalar import Call
 from ..kernels import AttentionKernel, Bind
 from .hip_backend import (_IDENTITY, _OP, STORAGE, WAVE, LaunchSpec, Renderer, _RowOffsets,
                           _expr_varies, _params, _reciprocal_divisors, _reciprocal_lines,
-                          _row_col_access, _scalar_division, axis_terms, cast_code,
-                          compute_type, index_type, join_offset, render_terms)
+                          _row_col_access, _scalar_division, axis_terms, bind_defs, cast_code,
+                          compute_type, half_inputs, index_type, join_offset, render_terms)
 from .reduction_schedule import varies_by_column
 
 #: the softmax's exp and its division by the row sum in fast forms
@@ -81,9 +82,19 @@ def attention_waves(heads: int, queries: int) -> int:
 
 
 class _FastExpRenderer(Renderer):
+    """``exp`` as ``mlc::exp_fast``; ``exp(a - b)`` as ``mlc::exp_fast_shift``
+    (one fma forms ``a log2 e - RN(b log2 e)``: with ``b`` a row's maximum the
+    rounding of ``b log2 e`` is the same factor on every exp of the row and
+    cancels in the normalisation)."""
+
     def call(self, e):
         if e.fn == "exp":
-            code, t = self(e.args[0])
+            x = e.args[0]
+            if isinstance(x, Call) and x.fn == "sub":
+                (a, ta), (b, tb) = self(x.args[0]), self(x.args[1])
+                if ta == "float" and tb == "float":
+                    return f"mlc::exp_fast_shift({a}, {b})", "float"
+            code, t = self(x)
             if t == "float":
                 return f"mlc::exp_fast({code})", "float"
         return super().call(e)
@@ -195,6 +206,23 @@ def _tile_of_workgroup(BH: int, NQB: int, QB: int, it: str) -> list[str]:
             f"  const int q0 = (int)(blockIdx.x % {NQB}) * {QB};"]
 
 
+def _round_scores(acc: str, dst: str, dtype: torch.dtype, ind: str) -> list[str]:
+    """A score tile's four fp32 accumulators rounded to the scores' storage
+    dtype, as the unfused schedule stores them. fp16 rounds the four in two
+    packed conversions; the fp32 copies read back are what the softmax's
+    mixed-precision fmas take in as fp16 operands. (Pairs, not the four at
+    once: a pair converts with one v_cvt_pk_f16_f32.)"""
+    if dtype == torch.float16:
+        return [f"{ind}{{ const mlc::half2v h0 = __builtin_convertvector("
+                f"(mlc::float2v){{{acc}[0], {acc}[1]}}, mlc::half2v);",
+                f"{ind}  const mlc::half2v h1 = __builtin_convertvector("
+                f"(mlc::float2v){{{acc}[2], {acc}[3]}}, mlc::half2v);",
+                f"{ind}  {dst}[0] = (float)h0[0]; {dst}[1] = (float)h0[1];",
+                f"{ind}  {dst}[2] = (float)h1[0]; {dst}[3] = (float)h1[1]; }}"]
+    return ["#pragma unroll",
+            f"{ind}for (int i = 0; i < 4; ++i) {dst}[i] = {cast_code(acc + '[i]', dtype)[0]};"]
+
+
 def _aligned(offset: int, strides) -> bool:
     return offset % 8 == 0 and all(s % 8 == 0 for s in strides)
 
@@ -273,8 +301,7 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     L.append(f"      const v8 kf = *reinterpret_cast<const v8*>(ks + (t * 16 + ql) * {PK} + dc * 32 + g * 8);")
     L.append("      acc = mlc::mfma_16x16x32(kf, qf[dc], acc);")
     L.append("    }")
-    L.append("#pragma unroll")
-    L.append(f"    for (int i = 0; i < 4; ++i) s[t][i] = {cast_code('acc[i]', k.score_dtype)[0]};")
+    L += _round_scores("acc", "s[t]", k.score_dtype, "    ")
     L.append("  }")
     L.append(f"  const {it} row = bh * ({it}){T} + ({it})(qw + ql);")
 
@@ -334,8 +361,9 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
         return name, temp_types[name]
 
     R_ = _FastExpRenderer if FAST_SOFTMAX_MATH else Renderer
-    elem_r = R_(ref_elem, temp_elem)
-    scal_r = R_(ref_scalar, temp_scalar)
+    half, defs = half_inputs(sm), bind_defs(sm)
+    elem_r = R_(ref_elem, temp_elem, half, defs)
+    scal_r = R_(ref_scalar, temp_scalar, half, defs)
     rcp_for = _reciprocal_divisors(sm, vector)
     score_cols = set(col_slots) | {k.score_slot}
 
@@ -535,6 +563,8 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append(f"  for (int dc = 0; dc < {D // 32}; ++dc)")
     L.append(f"    qf[dc] = *reinterpret_cast<const v8*>(qs + (w * 16 + ql) * {PQ} + dc * 32 + g * 8);")
     L.append("  float m_run = (-__builtin_huge_valf()), l_run = 0.0f;")
+    if FAST_SOFTMAX_MATH:
+        L.append("  float ml_run = (-__builtin_huge_valf());  // RN(m_run log2 e)")
     L.append(f"  mlc::float4v o[{D // 16}];")
     L.append("#pragma unroll")
     L.append(f"  for (int dt = 0; dt < {D // 16}; ++dt) o[dt] = mlc::float4v{{0.0f, 0.0f, 0.0f, 0.0f}};")
@@ -576,7 +606,8 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
         return name, temp_types[name]
 
     R_ = _FastExpRenderer if FAST_SOFTMAX_MATH else Renderer
-    elem_r, scal_r = R_(ref_elem, temp_elem), R_(ref_scalar, temp_scalar)
+    half, defs = half_inputs(sm), bind_defs(sm)
+    elem_r, scal_r = R_(ref_elem, temp_elem, half, defs), R_(ref_scalar, temp_scalar, half, defs)
     deps = dependencies(sm.steps)
     needed = deps[online.max_step.name]
     by_name = {s.name: s for s in sm.steps}
@@ -642,9 +673,9 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("      }")
     L.append(f"      float s[{NT}][4];")
     L.append("#pragma unroll")
-    L.append(f"      for (int t = 0; t < {NT}; ++t)")
-    L.append("#pragma unroll")
-    L.append(f"        for (int i = 0; i < 4; ++i) s[t][i] = {cast_code('acc[t][i]', k.score_dtype)[0]};")
+    L.append(f"      for (int t = 0; t < {NT}; ++t) {{")
+    L += _round_scores("acc[t]", "s[t]", k.score_dtype, "        ")
+    L.append("      }")
     # the other column operands (the mask): widened from the words loaded one
     # block ahead, then the next block's words are requested, so their memory
     # latency overlaps this block's work as the K/V tiles' does
@@ -693,21 +724,35 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
         L.append(f"        for (int m = 0; m < {NT // 2}; ++m)")
         L.append(f"          va[dt][m] = *reinterpret_cast<const v8*>(vt + (dt * 16 + ql) * {PV} + g * 8 + m * 32);  // keys vperm-ed")
     L.append("      const float m_new = mlc::max_<float>(m_run, mb);")
-    L.append(f"      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : {exp_}(m_run - m_new);")
-    L.append("      // a row with no finite score yet subtracts 0: its x are all -inf, exp gives 0")
-    L.append("      const float m_sub = m_new == (-__builtin_huge_valf()) ? 0.0f : m_new;")
+    if FAST_SOFTMAX_MATH:
+        # exponents in log2 units against the rounded RN(m log2 e): every exp
+        # and every rescale of the row uses the same rounded values, so
+        # their rounding is one common factor of o and l and cancels in o / l
+        L.append("      const float ml_new = m_new * 0x1.715476p+0f;")
+        L.append("      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f "
+                 ": __builtin_amdgcn_exp2f(ml_run - ml_new);")
+        L.append("      // a row with no finite score yet subtracts 0: its x are all -inf, exp gives 0")
+        L.append("      const float ml_sub = m_new == (-__builtin_huge_valf()) ? 0.0f : ml_new;")
+        exp_term = "__builtin_amdgcn_exp2f(__builtin_fmaf(x[t][i], 0x1.715476p+0f, -ml_sub))"
+    else:
+        L.append(f"      const float alpha = (m_run == (-__builtin_huge_valf())) ? 0.0f : {exp_}(m_run - m_new);")
+        L.append("      // a row with no finite score yet subtracts 0: its x are all -inf, exp gives 0")
+        L.append("      const float m_sub = m_new == (-__builtin_huge_valf()) ? 0.0f : m_new;")
+        exp_term = f"{exp_}(x[t][i] - m_sub)"
     L.append(f"      v4 p[{NT}];")
     L.append("      float psum = 0.0f;")
     L.append("#pragma unroll")
     L.append(f"      for (int t = 0; t < {NT}; ++t)")
     L.append("#pragma unroll")
     L.append("        for (int i = 0; i < 4; ++i) {")
-    L.append(f"          const float e = {exp_}(x[t][i] - m_sub);")
+    L.append(f"          const float e = {exp_term};")
     L.append("          psum += e;")
     L.append(f"          p[t][i] = (e16)e;")
     L.append("        }")
     L.append("      l_run = l_run * alpha + psum;")
     L.append("      m_run = m_new;")
+    if FAST_SOFTMAX_MATH:
+        L.append("      ml_run = ml_new;")
     L.append(f"      v8 bq[{NT // 2}];")
     L.append("#pragma unroll")
     L.append(f"      for (int m = 0; m < {NT // 2}; ++m)")

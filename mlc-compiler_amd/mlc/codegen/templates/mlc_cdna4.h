@@ -73,6 +73,8 @@ template <class S, class X> __device__ __forceinline__ void st(S* p, X x) { *p =
 // value rounded through a narrow float type, as a cast inside a kernel body
 // MFMA operand/accumulator fragments and a 16-byte bit copy of 8 halfs
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -153,6 +155,14 @@ __device__ __forceinline__ float exp_(float x) { return expf(x); }
 // (where exp(x) > 2e-9), two hundred times below fp16's half ulp.
 __device__ __forceinline__ float exp_fast(float x) {
   return __builtin_amdgcn_exp2f(x * 0x1.715476p+0f);
+}
+// exp(a - b) for the same use, with b a row's maximum: 2^(a log2 e - RN(b log2 e))
+// in one fma. The rounding of b log2 e multiplies every exp of the row by the
+// same factor, which cancels when the row is normalised by its sum; what is
+// left is the fma's one rounding of the exponent, as in exp_fast. Infinities
+// and NaN come out as for exp(a - b) (-inf - -inf is NaN, a - +inf is -inf).
+__device__ __forceinline__ float exp_fast_shift(float a, float b) {
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(a, 0x1.715476p+0f, -(b * 0x1.715476p+0f)));
 }
 // exp(x) for x <= 0, -inf or NaN: a softmax's exp(x - rowmax(x)).
 // h = RN(x log2 e) goes to v_exp_f32 whole, and the rounding of h is put back

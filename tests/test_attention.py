@@ -259,7 +259,9 @@ def test_long_rows_use_the_key_blocked_kernel():
     spec = mod.launches[att[0].name]
     assert spec.meta["mode"] == "blocked" and spec.meta["key_block"] == 64
     body = mod.functions[spec.symbol]
-    assert "m_run" in body and "l_run" in body and "mlc::exp_fast" in body
+    assert "m_run" in body and "l_run" in body and "ml_run" in body
+    # exponents in log2 units against the rounded RN(m log2 e): one fma each
+    assert "__builtin_amdgcn_exp2f(__builtin_fmaf(x[t][i], 0x1.715476p+0f, -ml_sub))" in body
     assert body.count("__syncthreads();") == 3
     assert sched.arena_bytes < base.arena_bytes // 2
 
