@@ -19,7 +19,8 @@ queries):
   storage dtype, as the unfused schedule stores them.
 * **row reduction**: the reduction kernel's own steps are rendered per
   element; each query's row lives in four lanes (``l % 16`` fixed), so a
-  reduce is a lane-local loop plus two ``__shfl_xor`` (16, 32).
+  reduce is a lane-local loop plus two lane exchanges (xor 16 and 32, on
+  ``v_permlane16_swap`` / ``v_permlane32_swap``).
 * **values**: ``O^T = V^T P^T`` on the same MFMA. The score layout of lane
   ``l`` is exactly the B fragment of ``P^T`` when the 32-element k axis of an
   MFMA pairs two 16-key tiles, so probabilities never leave registers. The
@@ -407,8 +408,11 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
         L.append(f"    for (int t = 0; t < {NT}; ++t)")
         L.append("#pragma unroll")
         L.append(f"      for (int i = 0; i < 4; ++i) acc = {op}::f(acc, ({t})({code}));")
-        L.append(f"    acc = {op}::f(acc, __shfl_xor(acc, 16, 64));")
-        L.append(f"    acc = {op}::f(acc, __shfl_xor(acc, 32, 64));")
+        if t == "float":
+            L.append(f"    acc = mlc::xor32<{op}>(mlc::xor16<{op}>(acc));")
+        else:
+            L.append(f"    acc = {op}::f(acc, __shfl_xor(acc, 16, 64));")
+            L.append(f"    acc = {op}::f(acc, __shfl_xor(acc, 32, 64));")
         L.append(f"    {st.name} = acc;")
         L.append("  }")
         L += _reciprocal_lines(st.name, rcp_for)
@@ -709,8 +713,7 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append(f"          x[t][i] = (float)({xcode});")
     L.append("          mb = mlc::max_<float>(mb, x[t][i]);")
     L.append("        }")
-    L.append("      mb = mlc::max_<float>(mb, __shfl_xor(mb, 16, 64));")
-    L.append("      mb = mlc::max_<float>(mb, __shfl_xor(mb, 32, 64));")
+    L.append("      mb = mlc::xor32<mlc::OpMax>(mlc::xor16<mlc::OpMax>(mb));")
     L.append("      // a block whose scores are all -inf for every row of the wave (a causal")
     L.append("      // mask's upper triangle) adds exactly nothing: skip its exp and P.V")
     L.append("      if (!__all(mb == (-__builtin_huge_valf()))) {")
@@ -787,8 +790,7 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("    __syncthreads();")
     L.append("  }")
     L.append("  if (!active) return;")
-    L.append("  l_run += __shfl_xor(l_run, 16, 64);")
-    L.append("  l_run += __shfl_xor(l_run, 32, 64);")
+    L.append("  l_run = mlc::xor32<mlc::OpSum>(mlc::xor16<mlc::OpSum>(l_run));")
     div = "* inv" if FAST_SOFTMAX_MATH else "/ l_run"
     if FAST_SOFTMAX_MATH:
         L.append("  const float inv = 1.0f / l_run;")

@@ -358,6 +358,23 @@ constexpr int kSwizzleXor16 = 0x401F; // bit-mask mode: and 0x1f, or 0, xor 0x10
 
 // Reduce over aligned groups of G lanes (G a power of two <= 64); every lane
 // of a group ends with the same value.
+// x combined by Op with the value of lane (lane ^ 16) (xor16) or (lane ^ 32)
+// (xor32) of the wave, on gfx950's v_permlane16_swap / v_permlane32_swap: a
+// VALU lane exchange with no LDS round trip. Each lane receives its own value
+// and its partner's, in one order or the other, so Op must be commutative
+// (sum, product, max and min are, exactly, in IEEE arithmetic). Every lane of
+// the wave must be active.
+template <class Op> __device__ __forceinline__ float xor16(float x) {
+  const unsigned v = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return Op::f(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+template <class Op> __device__ __forceinline__ float xor32(float x) {
+  const unsigned v = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return Op::f(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+
 template <int G, class Op>
 __device__ __forceinline__ float group_reduce(float x) {
   if constexpr (G >= 2) x = Op::f(x, dpp<kQuadSwap1>(x));
