@@ -306,6 +306,7 @@ def main() -> int:
                            ("fused_attention", "C2", ATTENTION),
                            ("fused_attention", "C4", ATTENTION),
                            ("all + fused_attention", "C2", ALL),
+                           ("all + fused_attention", "C3", ALL),
                            ("all + fused_attention", "C4", ALL),
                            # GPT-2 b32 s512 (config 5): the key-blocked attention kernel
                            ("gpt2_b32_s512", "C5", Config()),
@@ -324,7 +325,7 @@ def main() -> int:
         if key == "C5":
             slot = "all + fused_attention" if cfg.fused_attention else "reference"
         else:
-            slot = "b1" if key == "C2" else "b32"
+            slot = {"C2": "b1", "C3": "gpt2_b1", "C4": "b32"}[key]
         variants.setdefault(name, {})[slot] = entry
         del compiled, model, inputs
         torch.cuda.empty_cache()

@@ -37,7 +37,7 @@ DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()
            ("C5", Config(layout_selection=True)),
            ("C4", Config(layout_selection=True, gemm_epilogue=True)),
            ("C2", FAST), ("C4", FAST), ("C2", ATTENTION), ("C3", ATTENTION),
-           ("C4", ATTENTION), ("C5", ATTENTION), ("C2", ALL), ("C4", ALL),
+           ("C4", ATTENTION), ("C5", ATTENTION), ("C2", ALL), ("C3", ALL), ("C4", ALL),
            ("C5", ALL)]
 
 
