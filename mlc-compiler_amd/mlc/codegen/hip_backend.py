@@ -20,7 +20,7 @@ The MI355X design:
 * **persistent reduction**: each row is owned by G lanes (a power of two);
   lane ``l`` holds columns ``(k*G + l)*V .. +V`` for ``k < K`` in VGPRs, so a
   row is read once with coalesced 128-bit loads. Rows of <= 64 lanes reduce
-  with DPP/swizzle/readlane inside the wave and several rows share a
+  with DPP and v_permlane16/32_swap inside the wave and several rows share a
   workgroup; wider rows span whole waves and combine through LDS.
 * **streamed reduction** (rows longer than ``max_persistent_row``): one row
   per 256-thread workgroup, one chunked pass over HBM per reduce (or one

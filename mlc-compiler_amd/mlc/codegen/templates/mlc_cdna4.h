@@ -6,10 +6,10 @@
 //    with round-to-nearest-even on store;
 //  * the pointwise driver: one thread per V-element pack over a flat space;
 //  * wave64 cross-lane reductions for groups of 2..64 lanes using DPP
-//    (quad_perm, row_half_mirror, row_mirror), ds_swizzle (xor 16 within a
-//    32-lane half) and v_readlane (the two 32-lane halves), giving every lane
-//    of the group the bit-identical result; groups wider than a wave combine
-//    per-wave partials through LDS in a fixed order;
+//    (quad_perm, row_half_mirror, row_mirror) and gfx950's v_permlane16_swap /
+//    v_permlane32_swap (xor 16 and xor 32, VALU exchanges with no LDS round
+//    trip), giving every lane of the group the bit-identical result; groups
+//    wider than a wave combine per-wave partials through LDS in a fixed order;
 //  * scalar math helpers with torch semantics (NaN-propagating max/min,
 //    correctly rounded division, integer true division); transcendentals
 //    are ROCm's device math library, except erf and a softmax's exp of a
@@ -330,7 +330,7 @@ struct OpMin {
 };
 
 // ---------------------------------------------------------------------------
-// cross-lane movement (32-bit payloads through DPP / swizzle / readlane;
+// cross-lane movement (32-bit payloads through DPP and the permlane swaps;
 // 64-bit payloads through ds_bpermute shuffles)
 // ---------------------------------------------------------------------------
 template <int CTRL> __device__ __forceinline__ float dpp(float x) {
@@ -340,21 +340,11 @@ template <int CTRL> __device__ __forceinline__ float dpp(float x) {
 template <int CTRL> __device__ __forceinline__ int dpp(int x) {
   return __builtin_amdgcn_update_dpp(x, x, CTRL, 0xf, 0xf, false);
 }
-template <int PATTERN> __device__ __forceinline__ float swizzle(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), PATTERN));
-}
-template <int PATTERN> __device__ __forceinline__ int swizzle(int x) {
-  return __builtin_amdgcn_ds_swizzle(x, PATTERN);
-}
-__device__ __forceinline__ float readlane(float x, int lane) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
-}
 
 constexpr int kQuadSwap1 = 0xB1;     // quad_perm [1,0,3,2]
 constexpr int kQuadSwap2 = 0x4E;     // quad_perm [2,3,0,1]
 constexpr int kRowHalfMirror = 0x141;
 constexpr int kRowMirror = 0x140;
-constexpr int kSwizzleXor16 = 0x401F; // bit-mask mode: and 0x1f, or 0, xor 0x10
 
 // Reduce over aligned groups of G lanes (G a power of two <= 64); every lane
 // of a group ends with the same value.
@@ -362,8 +352,9 @@ constexpr int kSwizzleXor16 = 0x401F; // bit-mask mode: and 0x1f, or 0, xor 0x10
 // (xor32) of the wave, on gfx950's v_permlane16_swap / v_permlane32_swap: a
 // VALU lane exchange with no LDS round trip. Each lane receives its own value
 // and its partner's, in one order or the other, so Op must be commutative
-// (sum, product, max and min are, exactly, in IEEE arithmetic). Every lane of
-// the wave must be active.
+// (sum, product, max and min are, exactly, in IEEE arithmetic). A lane's
+// partner must be active whenever the lane is: true when whole aligned groups
+// of 32 (xor16) or 64 (xor32) lanes are active or inactive together.
 template <class Op> __device__ __forceinline__ float xor16(float x) {
   const unsigned v = __builtin_bit_cast(unsigned, x);
   const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
@@ -381,8 +372,8 @@ __device__ __forceinline__ float group_reduce(float x) {
   if constexpr (G >= 4) x = Op::f(x, dpp<kQuadSwap2>(x));
   if constexpr (G >= 8) x = Op::f(x, dpp<kRowHalfMirror>(x));
   if constexpr (G >= 16) x = Op::f(x, dpp<kRowMirror>(x));
-  if constexpr (G >= 32) x = Op::f(x, swizzle<kSwizzleXor16>(x));
-  if constexpr (G >= 64) x = Op::f(readlane(x, 0), readlane(x, 32));
+  if constexpr (G >= 32) x = xor16<Op>(x);
+  if constexpr (G >= 64) x = xor32<Op>(x);
   return x;
 }
 
