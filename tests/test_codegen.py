@@ -309,3 +309,33 @@ def test_mixed_precision_forms():
     # fp32 operands keep the plain operators
     body = _body(SubMul(), torch.randn(64, 256), torch.randn(64, 256))
     assert "one_()" not in body and "neg_zero_()" not in body
+
+
+def test_only_a_softmax_sum_drops_the_range_guard():
+    """A sum of exp(x - c) with a constant c is not a softmax row sum: it can
+    be 0 or overflow, so its division keeps the guarded fast path."""
+    class ShiftedByConstant(torch.nn.Module):
+        def forward(self, x):
+            e = torch.exp(x - 3.0)
+            return e / e.sum(dim=-1, keepdim=True)
+
+    body = _body(ShiftedByConstant(), torch.randn(8, 128).half())
+    assert "__all(ok_" in body and "mlc::exp_nonpos(" not in body
+
+
+def test_reciprocal_product_needs_a_16bit_rounding():
+    """The quotient becomes the reciprocal product only when it reaches
+    nothing but a rounding to fp16/bf16: a bf16 softmax uses it, an fp32 one
+    stays correctly rounded, and an fp16 one whose fp32 probabilities also
+    feed a sum keeps the correctly rounded quotient."""
+    s, m = torch.randn(4, 2, 16, 128), torch.zeros(4, 1, 1, 128)
+    assert "* rcp_" in _body(_ScaledMaskedSoftmax(), s.bfloat16(), m.bfloat16())
+    assert "* rcp_" not in _body(_ScaledMaskedSoftmax(), s, m)
+
+    class SoftmaxAndItsSum(torch.nn.Module):
+        def forward(self, x):
+            p = torch.softmax(x.float(), dim=-1)
+            return p.half(), p.sum(dim=-1)
+
+    body = _body(SoftmaxAndItsSum(), torch.randn(8, 128).half())
+    assert "mlc::div_rcp_finite(" in body and "* rcp_" not in body
