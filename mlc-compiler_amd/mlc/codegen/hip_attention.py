@@ -42,7 +42,7 @@ from __future__ import annotations
 
 import torch
 
-from ..ir.scalar import Call
+from ..ir.scalar import Call, Ref
 from ..kernels import AttentionKernel, Bind
 from .hip_backend import (_IDENTITY, _OP, STORAGE, WAVE, LaunchSpec, Renderer, _RowOffsets,
                           _expr_varies, _params, _reciprocal_divisors, _reciprocal_lines,
@@ -91,6 +91,8 @@ class _FastExpRenderer(Renderer):
     def call(self, e):
         if e.fn == "exp":
             x = e.args[0]
+            if isinstance(x, Ref) and isinstance(self.defs.get(x.name), Call):
+                x = self.defs[x.name]  # a bind holding the difference
             if isinstance(x, Call) and x.fn == "sub":
                 (a, ta), (b, tb) = self(x.args[0]), self(x.args[1])
                 if ta == "float" and tb == "float":
