@@ -989,7 +989,8 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
 
     nonpos = nonpositive_args(k)
     half_slots, defs, to_fp16 = half_inputs(k), bind_defs(k), fp16_rounded(k)
-    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos, half_slots, defs, to_fp16)
+    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos, half_slots, defs, to_fp16,
+                                fast_softmax_exps(k, nonpos))
     scal_r = Renderer(ref_scalar, temp_scalar, half_slots, defs, to_fp16)
     rcp_for = _reciprocal_divisors(k, vector)
 
@@ -1172,13 +1173,74 @@ def _row_division(k: ReductionKernel, name: str, num_expr: Expr, num: str, d: st
     return f"mlc::{div}({num}, {d}, rcp_{d})"
 
 
+def fast_softmax_exps(k: ReductionKernel, nonpos) -> frozenset[str]:
+    """Binds ``e = exp(x - rowmax(x))`` of a softmax whose probabilities reach
+    nothing but a rounding to fp16/bf16: ``e`` is read only by its row sum and
+    by divisions ``e / sum``, the sum only by those divisions, and every
+    quotient is storage-rounded (``storage_rounded``).
+
+    Such an exp may be ``mlc::exp_fast_shift(x, rowmax)``, one fma and
+    ``v_exp_f32``: the rounding of ``rowmax·log2 e`` is a common factor of the
+    numerators and of their sum, so it cancels in the quotient, and what is
+    left is the fma's one rounding of the exponent, about 1.2e-6 relative for
+    exponents up to 20 in size, against fp16's half ulp of 4.9e-4 that the
+    storage rounding adds (the attention kernels' softmax is written the same
+    way, for the same reason)."""
+    steps = {s.name: s for s in k.steps}
+    found = set()
+    for s in k.steps:
+        if not (isinstance(s, Reduce) and isinstance(s.expr, Ref) and softmax_sum(k, s.name, nonpos)):
+            continue
+        e_name, total = s.expr.name, Ref(s.name)
+        e_ref = Ref(e_name)
+        bind = steps.get(e_name)
+        if not (isinstance(bind, Bind) and isinstance(bind.expr, Call) and bind.expr.fn == "exp"):
+            continue
+        arg = bind.expr.args[0]
+        arg = steps[arg.name].expr if isinstance(arg, Ref) and isinstance(steps.get(arg.name), Bind) else arg
+        if not (isinstance(arg, Call) and arg.fn == "sub" and bind.expr.args[0] in nonpos):
+            continue
+        quotient = Call("div", (e_ref, total))
+        ok = True
+        divisions = []
+        for st in k.steps:
+            if st.name in (s.name, e_name):
+                continue
+            uses = set(_subexprs(st.expr))
+            if total in uses or e_ref in uses:
+                if isinstance(st, Bind) and st.expr == quotient and storage_rounded(k, st.name):
+                    divisions.append(st.name)
+                else:
+                    ok = False
+        for a in k.outputs:
+            uses = set(_subexprs(k.out_expr[a.value.name]))
+            if total in uses or e_ref in uses:
+                ok = False
+        if ok and divisions:
+            found.add(e_name)
+    return frozenset(found)
+
+
 class _NonPosExpRenderer(Renderer):
-    """``exp`` of an argument known to be at most 0 as ``mlc::exp_nonpos``."""
+    """``exp`` of an argument known to be at most 0 as ``mlc::exp_nonpos``;
+    the binds of ``fast`` (``fast_softmax_exps``) as
+    ``mlc::exp_fast_shift(x, rowmax)``."""
 
     def __init__(self, operand, temp, nonpos: set, half_slots=frozenset(), defs=None,
-                 to_fp16=frozenset()) -> None:
+                 to_fp16=frozenset(), fast=frozenset()) -> None:
         super().__init__(operand, temp, half_slots, defs, to_fp16)
         self.nonpos = nonpos
+        self.fast = frozenset(fast)
+
+    def bind(self, name: str, e: Expr) -> tuple[str, str]:
+        if name in self.fast:
+            arg = e.args[0]
+            if isinstance(arg, Ref):
+                arg = self.defs[arg.name]
+            (x, tx), (m, tm) = self(arg.args[0]), self(arg.args[1])
+            if tx == "float" and tm == "float":
+                return f"mlc::exp_fast_shift({x}, {m})", "float"
+        return super().bind(name, e)
 
     def call(self, e: Call) -> tuple[str, str]:
         if e.fn == "exp" and e.args[0] in self.nonpos:

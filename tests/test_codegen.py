@@ -254,6 +254,27 @@ def test_softmax_division_by_a_row_sum():
     assert "mlc::div_rcp_finite(" in b32 and "__all(ok_" not in b32
 
 
+def test_fp16_softmax_uses_the_shifted_fast_exp():
+    """A softmax whose probabilities are only stored as fp16 computes its exp
+    as ``exp_fast_shift(x, rowmax)`` (the rounding of rowmax·log2 e cancels in
+    the normalisation); an fp32 softmax, or one whose row sum is also an
+    output, keeps the accurate ``exp_nonpos``."""
+    s, m = torch.randn(4, 2, 16, 128), torch.zeros(4, 1, 1, 128)
+    b16 = _body(_ScaledMaskedSoftmax(), s.half(), m.half())
+    assert "mlc::exp_fast_shift(" in b16 and "mlc::exp_nonpos(" not in b16
+    b32 = _body(_ScaledMaskedSoftmax(), s, m)
+    assert "mlc::exp_nonpos(" in b32 and "exp_fast" not in b32
+
+    class SoftmaxAndDenominator(torch.nn.Module):
+        def forward(self, x):
+            e = torch.exp(x - x.amax(dim=-1, keepdim=True))
+            d = e.sum(dim=-1, keepdim=True)
+            return (e / d).half(), d
+
+    body = _body(SoftmaxAndDenominator(), torch.randn(8, 128))
+    assert "mlc::exp_nonpos(" in body and "exp_fast" not in body
+
+
 def test_other_row_divisions_keep_the_range_guard():
     """A division by a row statistic that is not a softmax sum (here a sum of
     squares, which can be 0 or huge) keeps the guarded fast path and the IEEE
