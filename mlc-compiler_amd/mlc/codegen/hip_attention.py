@@ -8,24 +8,26 @@ queries):
 * **staging**: the block's queries, and every key and value of the head,
   are copied from their strided views into LDS with 128-bit loads along
   whichever axis is unit-stride, all loads issued before the first LDS
-  store. K is kept as ``[key][d]`` and V transposed
-  as ``[d][key]``; row pitches are padded by 8 elements so the 16-lane phases
-  of ``ds_read_b128`` hit distinct banks.
+  store. K is kept as ``[key][d]``, its rows in the order ``mlc::krow``
+  gives, and V transposed as ``[d][key]``; row pitches are padded by 8
+  elements so the 16-lane phases of ``ds_read_b128`` hit distinct banks.
 * **scores**: each wave owns 16 queries and computes ``S^T = K Q^T`` with
   ``v_mfma_f32_16x16x32_f16`` (``_bf16`` for bf16 heads; the body is written
-  once over the ``e16``/``v8``/``v4`` aliases) -- A = a 16-key tile of K, B = the wave's Q
-  fragment (read once) -- so lane ``l`` ends up holding query ``l % 16``'s
-  scores for keys ``16 t + 4 (l / 16) + i``. Scores are rounded to their
-  storage dtype, as the unfused schedule stores them.
+  once over the ``e16``/``v8``/``v4`` aliases) -- A = a 16-key tile of K
+  (LDS rows ``16 t .. 16 t + 15``), B = the wave's Q fragment (read once) --
+  so lane ``l`` ends up holding query ``l % 16``'s scores for keys
+  ``32 (t / 2) + 8 (l / 16) + 4 (t % 2) + i``: eight consecutive keys of
+  every 32-key chunk, whose mask words are one 16-byte load. Scores are
+  rounded to their storage dtype, as the unfused schedule stores them.
 * **row reduction**: the reduction kernel's own steps are rendered per
   element; each query's row lives in four lanes (``l % 16`` fixed), so a
   reduce is a lane-local loop plus two lane exchanges (xor 16 and 32, on
   ``v_permlane16_swap`` / ``v_permlane32_swap``).
 * **values**: ``O^T = V^T P^T`` on the same MFMA. The score layout of lane
   ``l`` is exactly the B fragment of ``P^T`` when the 32-element k axis of an
-  MFMA pairs two 16-key tiles, so probabilities never leave registers. The
-  staged V^T tile stores each 32-key chunk in the key order ``mlc::vperm``
-  gives, so a lane's 8 A values are one 16-byte LDS read. Lane ``l`` ends
+  MFMA is one 32-key chunk (tiles ``2 m`` and ``2 m + 1``), in key order, so
+  probabilities never leave registers and a lane's 8 A values are one
+  16-byte read of the unpermuted V^T tile. Lane ``l`` ends
   with four consecutive head-dim values of query ``l % 16``: one 8-byte
   store each, at the output's index map over the flat ``[BH, T, D]`` index
   (identity, or the permutation of a folded context copy).
@@ -118,15 +120,15 @@ def _type_aliases(k: AttentionKernel) -> str:
 
 def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc: int, pr: int,
            pc: int, aligned_c: bool, aligned_r: bool, threads: int, rows_valid: str | None,
-           it: str, perm_r: bool = False) -> tuple[list[str], list[str]]:
+           it: str, key_rows: bool = False) -> tuple[list[str], list[str]]:
     """Copy the R x C tile ``src[base + r*sr + c*sc]`` to ``lds[r*pr + c*pc]``
-    (``lds[vperm(r) + c*pc]`` with ``perm_r``, for the V^T tile).
+    (``lds[krow(r)*pr + c*pc]`` with ``key_rows``, for the K tile: the key
+    order the score MFMAs read, ``mlc::krow``).
 
     Returns (load lines, store lines): every load of every operand is issued
     before the first LDS store, so the workgroup waits for memory once, not
     once per loop trip."""
-    assert not perm_r or pr == 1
-    rr = "mlc::vperm(r)" if perm_r else "r"
+    rr = "mlc::krow(r)" if key_rows else "r"
     load: list[str] = []
     store: list[str] = []
     if sc == 1 and C % 8 == 0 and aligned_c:
@@ -164,20 +166,14 @@ def _stage(tag: str, lds: str, src: str, base: str, R: int, C: int, sr: int, sc:
     if per == 8:
         load.append(f"    {guard}{tag}[u] = *reinterpret_cast<const v8*>({addr});")
         if mode == "c" and pc == 1 and pr % 8 == 0:
-            store.append(f"    {guard}*reinterpret_cast<v8*>({lds} + r * {pr} + c) = {tag}[u];")
-        elif mode == "r" and pr == 1 and pc % 8 == 0 and perm_r:
-            # 8 keys starting at a multiple of 8 land as two runs of 4
-            store.append(f"    {guard}{{")
-            store.append(f"      *reinterpret_cast<v4*>({lds} + mlc::vperm(r) + c * {pc}) = {tag}[u].lo;")
-            store.append(f"      *reinterpret_cast<v4*>({lds} + mlc::vperm(r + 4) + c * {pc}) = {tag}[u].hi;")
-            store.append("    }")
-        elif mode == "r" and pr == 1 and pc % 8 == 0:
+            store.append(f"    {guard}*reinterpret_cast<v8*>({lds} + {rr} * {pr} + c) = {tag}[u];")
+        elif mode == "r" and pr == 1 and pc % 8 == 0 and not key_rows:
             store.append(f"    {guard}*reinterpret_cast<v8*>({lds} + r + c * {pc}) = {tag}[u];")
         else:
             if mode == "c":  # one row, 8 columns
                 row, col = rr, "(c + j)"
             else:  # 8 rows, one column
-                row, col = ("mlc::vperm(r + j)" if perm_r else "(r + j)"), "c"
+                row, col = ("mlc::krow(r + j)" if key_rows else "(r + j)"), "c"
             store.append(f"    {guard}{{")
             store.append("#pragma unroll")
             store.append(f"      for (int j = 0; j < 8; ++j) {lds}[{row} * {pr} + {col} * {pc}] "
@@ -224,6 +220,32 @@ def _round_scores(acc: str, dst: str, dtype: torch.dtype, ind: str) -> list[str]
                 f"{ind}  {dst}[2] = (float)h1[0]; {dst}[3] = (float)h1[1]; }}"]
     return ["#pragma unroll",
             f"{ind}for (int i = 0; i < 4; ++i) {dst}[i] = {cast_code(acc + '[i]', dtype)[0]};"]
+
+
+def _lane_words(sm, a, dst: str, base: str, c0: str, offs, it: str, ind: str) -> list[str]:
+    """The 8 words of column operand ``a`` at keys ``c0 .. c0 + 7`` into
+    ``dst[0..7]``: one 16-byte load when the row's columns are unit-stride
+    and 16-byte aligned, two 8-byte loads at 8-byte alignment, else one load
+    per word. ``c0`` is a multiple of 8 (a lane's keys, ``mlc::krow``)."""
+    S = STORAGE[a.dtype]
+    out = [f"{ind}{{ const {it} c0 = ({it})({c0});"]
+    for V in (8, 4):
+        acc = _row_col_access(sm, a, V)
+        if acc.mode == "affine" and acc.aligned:
+            out.append("#pragma unroll")
+            out.append(f"{ind}  for (int h = 0; h < {8 // V}; ++h) {{")
+            out.append(f"{ind}    const mlc::pack<{S}, {V}> w_ = *reinterpret_cast<const mlc::pack<{S}, {V}>*>"
+                       f"({base} + {offs.col(a, f'(c0 + ({it})(h * {V}))')});")
+            out.append("#pragma unroll")
+            out.append(f"{ind}    for (int j = 0; j < {V}; ++j) {dst}[h * {V} + j] = w_.x[j];")
+            out.append(f"{ind}  }}")
+            break
+    else:
+        out.append("#pragma unroll")
+        out.append(f"{ind}  for (int j = 0; j < 8; ++j) {dst}[j] = "
+                   f"({base})[{offs.col(a, f'(c0 + ({it})j)')}];")
+    out.append(f"{ind}}}")
+    return out
 
 
 def _aligned(offset: int, strides) -> bool:
@@ -277,13 +299,13 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     ksb, ksd, ksk = kl.strides
     k_ld, k_st = _stage("gk", "ks", "in1", f"(({it}){kl.offset} + bh * ({it}){ksb})", Tk, D, ksk,
                         ksd, PK, 1, _aligned(kl.offset, (ksb, ksk)),
-                        _aligned(kl.offset, (ksb, ksd)), THREADS, None, it)
+                        _aligned(kl.offset, (ksb, ksd)), THREADS, None, it, key_rows=True)
     # v is [BH, Tk, D], staged transposed as [d][key]
     vl = k.v.layout
     vsb, vsk, vsd = vl.strides
     v_ld, v_st = _stage("gv", "vt", "in2", f"(({it}){vl.offset} + bh * ({it}){vsb})", Tk, D, vsk,
                         vsd, 1, PV, _aligned(vl.offset, (vsb, vsk)),
-                        _aligned(vl.offset, (vsb, vsd)), THREADS, None, it, perm_r=True)
+                        _aligned(vl.offset, (vsb, vsd)), THREADS, None, it)
     L += q_ld + k_ld + v_ld + q_st + k_st + v_st
     L.append("  __syncthreads();")
     L.append("  const int w = threadIdx.x / 64, l = threadIdx.x % 64;")
@@ -326,18 +348,17 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
         if i not in col_slots:
             L.append(f"  const {ct} x{i} = mlc::ld(in{p} + {offs.row(a)});")
             continue
-        acc = _row_col_access(sm, a, 4)
         L.append(f"  {ct} x{i}[{NT}][4];")
         L.append(f"  {{ const {it} rb = {offs.row(a)};")
         L.append("#pragma unroll")
-        L.append(f"    for (int t = 0; t < {NT}; ++t) {{")
-        L.append(f"      const {it} c0 = ({it})(t * 16 + g * 4);")
-        if acc.mode == "affine" and acc.aligned:
-            L.append(f"      mlc::load_pack<4>(x{i}[t], in{p} + rb + {offs.col(a, 'c0')});")
-        else:
-            L.append("#pragma unroll")
-            L.append(f"      for (int j = 0; j < 4; ++j) x{i}[t][j] = "
-                     f"mlc::ld(in{p} + rb + {offs.col(a, '(c0 + (' + it + ')j)')});")
+        L.append(f"    for (int m = 0; m < {NT // 2}; ++m) {{")
+        L.append(f"      {STORAGE[a.dtype]} w[8];")
+        L += _lane_words(sm, a, "w", f"in{p} + rb", "m * 32 + g * 8", offs, it, "      ")
+        L.append("#pragma unroll")
+        L.append("      for (int j = 0; j < 4; ++j) {")
+        L.append(f"        x{i}[2 * m][j] = mlc::ld(&w[j]);")
+        L.append(f"        x{i}[2 * m + 1][j] = mlc::ld(&w[4 + j]);")
+        L.append("      }")
         L.append("    }")
         L.append("  }")
 
@@ -429,7 +450,7 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
     L.append("#pragma unroll")
     L.append(f"  for (int dt = 0; dt < {D // 16}; ++dt) {{")
     L.append("    mlc::float4v o = {0.0f, 0.0f, 0.0f, 0.0f};")
-    L.append(f"    const e16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
+    L.append(f"    const e16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;")
     L.append("#pragma unroll")
     L.append(f"    for (int m = 0; m < {NT // 2}; ++m) {{")
     L.append("      const v8 a = *reinterpret_cast<const v8*>(vrow + m * 32);")
@@ -545,14 +566,14 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     k_ld, k_st = _stage("gk", "ks", "in1",
                         f"(({it}){kl.offset} + bh * ({it}){ksb} + ({it})kb0 * ({it}){ksk})",
                         KB, D, ksk, ksd, PK, 1, _aligned(kl.offset, (ksb, ksk, KB * ksk)),
-                        _aligned(kl.offset, (ksb, ksd, KB * ksk)), THREADS, None, it)
+                        _aligned(kl.offset, (ksb, ksd, KB * ksk)), THREADS, None, it,
+                        key_rows=True)
     vl = k.v.layout
     vsb, vsk, vsd = vl.strides
     v_ld, v_st = _stage("gv", "vt", "in2",
                         f"(({it}){vl.offset} + bh * ({it}){vsb} + ({it})kb0 * ({it}){vsk})",
                         KB, D, vsk, vsd, 1, PV, _aligned(vl.offset, (vsb, vsk, KB * vsk)),
-                        _aligned(vl.offset, (vsb, vsd, KB * vsk)), THREADS, None, it,
-                        perm_r=True)
+                        _aligned(vl.offset, (vsb, vsd, KB * vsk)), THREADS, None, it)
     # declarations hoisted out of the block loop
     L += q_ld + q_st
     L += [k_ld[0], v_ld[0]]
@@ -632,25 +653,17 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
         out = []
         for i in mask_slots:
             a = sm.inputs[i]
-            acc = _row_col_access(sm, a, 4)
-            p = param[i]
             out.append(f"{ind}{{ const {it} rb = {offs.row(a)};")
             out.append("#pragma unroll")
-            out.append(f"{ind}  for (int t = 0; t < {NT}; ++t) {{")
-            out.append(f"{ind}    const {it} c0 = ({it})({kc} + t * 16 + g * 4);")
-            if acc.mode == "affine" and acc.aligned:
-                out.append(f"{ind}    xr{i}[t] = *reinterpret_cast<const mlc::pack<{STORAGE[a.dtype]}, 4>*>"
-                           f"(in{p} + rb + {offs.col(a, 'c0')});")
-            else:
-                out.append("#pragma unroll")
-                out.append(f"{ind}    for (int j = 0; j < 4; ++j) xr{i}[t].x[j] = "
-                           f"in{p}[rb + {offs.col(a, '(c0 + (' + it + ')j)')}];")
+            out.append(f"{ind}  for (int m = 0; m < {NT // 2}; ++m) {{")
+            out += _lane_words(sm, a, f"xr{i}[m].x", f"in{param[i]} + rb",
+                               f"{kc} + m * 32 + g * 8", offs, it, ind + "    ")
             out.append(f"{ind}  }}")
             out.append(f"{ind}}}")
         return out
 
     for i in mask_slots:
-        L.append(f"  mlc::pack<{STORAGE[sm.inputs[i].dtype]}, 4> xr{i}[{NT}];")
+        L.append(f"  mlc::pack<{STORAGE[sm.inputs[i].dtype]}, 8> xr{i}[{NT // 2}];")
     if mask_slots:
         L.append("  if (active) {")
         L += mask_loads("0", "    ")
@@ -690,7 +703,7 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
         L.append("#pragma unroll")
         L.append(f"      for (int t = 0; t < {NT}; ++t)")
         L.append("#pragma unroll")
-        L.append(f"        for (int j = 0; j < 4; ++j) x{i}[t][j] = mlc::ld(&xr{i}[t].x[j]);")
+        L.append(f"        for (int j = 0; j < 4; ++j) x{i}[t][j] = mlc::ld(&xr{i}[t / 2].x[(t % 2) * 4 + j]);")
     if mask_slots:
         L.append(f"      if (b + 1 < {NB}) {{")
         L += mask_loads("(kc + " + str(KB) + ")", "        ")
@@ -727,7 +740,7 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
         L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt)")
         L.append("#pragma unroll")
         L.append(f"        for (int m = 0; m < {NT // 2}; ++m)")
-        L.append(f"          va[dt][m] = *reinterpret_cast<const v8*>(vt + (dt * 16 + ql) * {PV} + g * 8 + m * 32);  // keys vperm-ed")
+        L.append(f"          va[dt][m] = *reinterpret_cast<const v8*>(vt + (dt * 16 + ql) * {PV} + g * 8 + m * 32);")
     L.append("      const float m_new = mlc::max_<float>(m_run, mb);")
     if FAST_SOFTMAX_MATH:
         # exponents in log2 units against the rounded RN(m log2 e): every exp
@@ -776,7 +789,7 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     else:
         L.append("#pragma unroll")
         L.append(f"      for (int dt = 0; dt < {D // 16}; ++dt) {{")
-        L.append(f"        const e16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;  // keys vperm-ed")
+        L.append(f"        const e16* vrow = vt + (dt * 16 + ql) * {PV} + g * 8;")
         L.append("#pragma unroll")
         L.append(f"        for (int m = 0; m < {NT // 2}; ++m) {{")
         L.append("          const v8 a = *reinterpret_cast<const v8*>(vrow + m * 32);")

@@ -90,11 +90,14 @@ __device__ __forceinline__ float4v mfma_16x16x32(bf16x8 a, bf16x8 b, float4v c) 
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Key position inside a staged V^T row of the attention kernels: within each
-// 32-key chunk, key 16h + 4g + i sits at 8g + 4h + i, so the 8 keys one lane
-// feeds an MFMA (keys 4g..4g+3 of two 16-key tiles) are one 16-byte LDS read.
-__device__ __forceinline__ int vperm(int k) {
-  return (k & ~31) | (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
+// LDS row of key k in a staged K tile of the attention kernels. The score
+// MFMA of 16-key tile t reads LDS rows 16t..16t+15, and row 16t + r holds key
+// 32(t/2) + 8(r/4) + 4(t%2) + r%4: lane (q, g) then ends with keys
+// 32m + 8g .. 32m + 8g + 7 of every 32-key chunk m, so a lane's mask words are
+// 16 contiguous bytes and its probabilities are the P.V MFMA's B operand in
+// key order (V^T is staged unpermuted).
+__device__ __forceinline__ int krow(int k) {
+  return (k & ~31) | (((k >> 2) & 1) << 4) | (((k >> 3) & 3) << 2) | (k & 3);
 }
 
 __device__ __forceinline__ float round_f16(float x) { return static_cast<float>(static_cast<f16>(x)); }

@@ -202,10 +202,11 @@ def test_operand_producers_write_the_mfma_layouts():
         assert a.kt.layout.strides == (128 * 64, 1, 64)
         assert a.v.layout.strides == (128 * 64, 1, 128)
         body = mod.functions[mod.launches[a.name].symbol]
-        # Q and K: one 128-bit store per pack; V^T: two 64-bit stores at the
-        # key-permuted positions the 128-bit MFMA-operand reads expect
-        assert body.count("*reinterpret_cast<v8*>(") == 2 and "[u][j]" not in body
-        assert body.count("*reinterpret_cast<v4*>(vt + mlc::vperm(") == 2
+        # Q, K and V^T: one 128-bit LDS store per pack, K's rows in the key
+        # order the score MFMAs read (mlc::krow), V^T unpermuted
+        assert body.count("*reinterpret_cast<v8*>(") == 3 and "[u][j]" not in body
+        assert body.count("*reinterpret_cast<v8*>(ks + mlc::krow(r) * ") == 1
+        assert "*reinterpret_cast<v8*>(vt + r + c * " in body
         assert body.count("*reinterpret_cast<const v8*>(vrow") == 1
     assert not verify(list(sched.plan.live_ranges.values()), sched.plan.offsets)
 
