@@ -553,14 +553,31 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L += _tile_of_workgroup(BH, NQB, QB, it)
     ql_ = k.q.layout
     qsb, qsr, qsc = ql_.strides
-    rows_valid = None
-    if T % QB:
-        L.append(f"  const int qn = {T} - q0 < {QB} ? {T} - q0 : {QB};")
-        rows_valid = "qn"
-    q_ld, q_st = _stage("gq", "qs", "in0",
-                        f"(({it}){ql_.offset} + bh * ({it}){qsb} + ({it})q0 * ({it}){qsr})",
-                        QB, D, qsr, qsc, PQ, 1, _aligned(ql_.offset, (qsb, qsr)),
-                        _aligned(ql_.offset, (qsb, qsc)), THREADS, rows_valid, it)
+    # query tile j of a head holds the half-tiles j and 2 NQB - 1 - j (waves
+    # 0 .. W/2 - 1 and W/2 .. W - 1): under a causal mask every workgroup then
+    # has the same number of unmasked keys, so no late, long workgroup sets
+    # the kernel's end; any other mask is indifferent to the pairing
+    fold = T % QB == 0 and W % 2 == 0 and NQB > 1
+    if fold:
+        H = QB // 2
+        L.append(f"  const int qa = (q0 / {QB}) * {H}, qb = ({2 * NQB - 1} - q0 / {QB}) * {H};")
+        q_ld, q_st = [], []
+        for tag, lds, first in (("gq", "qs", "qa"), ("gq2", f"(qs + {H * PQ})", "qb")):
+            ld_, st_ = _stage(tag, lds, "in0",
+                              f"(({it}){ql_.offset} + bh * ({it}){qsb} + ({it}){first} * ({it}){qsr})",
+                              H, D, qsr, qsc, PQ, 1, _aligned(ql_.offset, (qsb, qsr)),
+                              _aligned(ql_.offset, (qsb, qsc)), THREADS, None, it)
+            q_ld += ld_
+            q_st += st_
+    else:
+        rows_valid = None
+        if T % QB:
+            L.append(f"  const int qn = {T} - q0 < {QB} ? {T} - q0 : {QB};")
+            rows_valid = "qn"
+        q_ld, q_st = _stage("gq", "qs", "in0",
+                            f"(({it}){ql_.offset} + bh * ({it}){qsb} + ({it})q0 * ({it}){qsr})",
+                            QB, D, qsr, qsc, PQ, 1, _aligned(ql_.offset, (qsb, qsr)),
+                            _aligned(ql_.offset, (qsb, qsc)), THREADS, rows_valid, it)
     kl = k.kt.layout
     ksb, ksd, ksk = kl.strides
     k_ld, k_st = _stage("gk", "ks", "in1",
@@ -582,7 +599,10 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
     L.append("  __syncthreads();")
     L.append("  const int w = threadIdx.x / 64, l = threadIdx.x % 64;")
     L.append("  const int ql = l % 16, g = l / 16;")
-    L.append("  const int qw = q0 + w * 16;")
+    if fold:
+        L.append(f"  const int qw = w < {W // 2} ? qa + w * 16 : qb + (w - {W // 2}) * 16;")
+    else:
+        L.append("  const int qw = q0 + w * 16;")
     L.append(f"  const bool active = qw < {T};  // wave-uniform; every wave meets every barrier")
     L.append(f"  const {it} row = bh * ({it}){T} + ({it})(active ? qw + ql : 0);")
     L.append(f"  v8 qf[{D // 32}];")

@@ -264,6 +264,10 @@ def test_long_rows_use_the_key_blocked_kernel():
     # exponents in log2 units against the rounded RN(m log2 e): one fma each
     assert "__builtin_amdgcn_exp2f(__builtin_fmaf(x[t][i], 0x1.715476p+0f, -ml_sub))" in body
     assert body.count("__syncthreads();") == 3
+    # 4 query tiles of 128 per head: tile j is the half-tiles j and 7 - j, so
+    # under the causal mask every workgroup has the same unmasked keys
+    assert "const int qa = (q0 / 128) * 64, qb = (7 - q0 / 128) * 64;" in body
+    assert "const int qw = w < 4 ? qa + w * 16 : qb + (w - 4) * 16;" in body
     assert sched.arena_bytes < base.arena_bytes // 2
 
 
