@@ -331,3 +331,42 @@ def test_common_attention_patterns_fuse(tk):
         exact = exact_attention(name, args)
         err = ((got.double() - exact).abs().max() / exact.abs().max()).item()
         assert err <= 2e-3, (name, err)
+
+
+class _OffsetMask(nn.Module):
+    """An additive fp16 mask read through a column slice at offset ``off``."""
+
+    def __init__(self, off):
+        super().__init__()
+        self.off = off
+
+    def forward(self, q, k, v, mask):
+        tk = k.shape[-2]
+        s = (q @ k.transpose(-2, -1)) / math.sqrt(q.shape[-1]) + mask[..., self.off:self.off + tk]
+        return s.softmax(-1) @ v
+
+
+def offset_mask_case(off, t=128, tk=128):
+    q, k, v, _ = _inputs(2, 2, t, tk, 64)
+    causal = torch.triu(torch.full((t, tk + 8), float("-inf")), diagonal=1 + off)
+    return _OffsetMask(off), (q, k, v, causal.to(torch.float16)[None, None])
+
+
+@pytest.mark.parametrize("tk", [128, 256])
+@pytest.mark.parametrize("off,form", [(0, "mlc::pack<mlc::f16, 8>"), (4, "mlc::pack<mlc::f16, 4>"),
+                                      (1, "for (int j = 0; j < 8; ++j)")])
+def test_mask_words_load_at_the_widest_aligned_width(off, form, tk):
+    """A lane's 8 mask words per 32-key chunk are one 16-byte load when the
+    mask's rows are 16-byte aligned, two 8-byte loads at 8-byte alignment
+    (a column slice at offset 4), and one load per word otherwise."""
+    model, args = offset_mask_case(off, tk, tk)
+    sched = build_pipeline(capture(model, args), ATTN)
+    mod = build_module(sched, ATTN)
+    att = _attention(sched)
+    assert len(att) == 1
+    body = mod.functions[mod.launches[att[0].name].symbol]
+    assert form in body
+    for wider in ("mlc::pack<mlc::f16, 8>", "mlc::pack<mlc::f16, 4>"):
+        if wider == form:
+            break
+        assert f"const {wider} w_" not in body

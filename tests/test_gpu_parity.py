@@ -673,6 +673,29 @@ def test_common_attention_patterns_on_the_gpu(tk):
         assert e_oracle <= 2e-3 and e_exact <= 2e-3, name
 
 
+@pytest.mark.parametrize("tk", [128, 256])
+@pytest.mark.parametrize("off", [0, 4, 1])
+def test_attention_mask_at_every_alignment(off, tk):
+    """The mask words loaded 16 bytes at a time (offset 0), 8 bytes at a time
+    (a column slice at offset 4) and one at a time (offset 1), in the
+    single-pass (128 keys) and key-blocked (256 keys) kernels: within 2e-3 of
+    the oracle's fused kernel and of float64."""
+    from test_attention import offset_mask_case
+
+    model, args = offset_mask_case(off, tk, tk)
+    want = compile_reference(model, args, ATTN)(*args)
+    exact = model(*(a.double() for a in args))
+    dev = tuple(a.cuda() for a in args)
+    compiled = mlc.compile(model, dev, ATTN)
+    assert [s.meta["kind"] for s in compiled._module.launch_table.values()].count("attention") == 1
+    got = compiled(*dev)
+    torch.cuda.synchronize()
+    e_oracle, e_exact = rel_err(got, want), rel_err(got, exact)
+    print(f"mask offset {off}, {tk} keys: hip-vs-oracle {e_oracle:.2e} hip-vs-fp64 {e_exact:.2e}")
+    assert torch.isfinite(got).all()
+    assert e_oracle <= 2e-3 and e_exact <= 2e-3
+
+
 class _Embed(torch.nn.Module):
     def __init__(self):
         super().__init__()
