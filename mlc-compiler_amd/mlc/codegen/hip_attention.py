@@ -201,6 +201,13 @@ def _tile_of_workgroup(BH: int, NQB: int, QB: int, it: str) -> list[str]:
         return [f"  const uint32_t xcd = blockIdx.x % {XCDS}, slot = blockIdx.x / {XCDS};",
                 f"  const {it} bh = ({it})((slot / {NQB}) * {XCDS} + xcd);",
                 f"  const int q0 = (int)(slot % {NQB}) * {QB};"]
+    if NQB > 1 and (BH * NQB) % XCDS == 0:
+        # XCD x takes a contiguous run of the (head, tile) list: a head's tiles
+        # span at most two XCDs
+        per = BH * NQB // XCDS
+        return [f"  const uint32_t item = (blockIdx.x % {XCDS}) * {per} + blockIdx.x / {XCDS};",
+                f"  const {it} bh = ({it})(item / {NQB});",
+                f"  const int q0 = (int)(item % {NQB}) * {QB};"]
     return [f"  const {it} bh = ({it})(blockIdx.x / {NQB});",
             f"  const int q0 = (int)(blockIdx.x % {NQB}) * {QB};"]
 
