@@ -41,6 +41,11 @@ class Config:
     #: model on the GPU that sets it, so their calls must not overlap)
     #: instead of a slab of its own. Changes no schedule.
     static_arena: bool = False
+    #: wait for every call to finish and raise ``ExecutionError`` in that
+    #: same call when it met an invalid input (an embedding id outside its
+    #: table). Costs one stream synchronize per call. Off: the error is
+    #: raised by the next call or by ``check_errors()``. Changes no schedule.
+    sync_input_checks: bool = False
 
     # codegen
     pointwise_block: int = 1024

@@ -363,6 +363,9 @@ class CompiledModel:
                 self.run_one(k, table)
                 for name in plan.free_at.get(i, ()):
                     table.pop(name, None)
+            fetch = getattr(self._module, "fetch_errors", None)
+            if fetch is not None:
+                fetch()
             return self._collect(table)
         table = self._buffers.resident(inputs)
         self._resolve(table)
@@ -372,14 +375,18 @@ class CompiledModel:
     def __call__(self, *inputs: torch.Tensor):
         self._raise_pending()
         if not (self.cfg.cuda_graphs and self.device.type == "cuda"):
-            return self.forward(*inputs)
-        if not self._captured:
-            self._capture(inputs)
-        self._check_inputs(inputs)
-        for dst, src in zip(self._buffers.inputs, inputs):
-            dst.copy_(src.reshape(-1), non_blocking=True)
-        self._module.replay(torch.cuda.current_stream(self.device).cuda_stream)
-        return self._static_outputs
+            out = self.forward(*inputs)
+        else:
+            if not self._captured:
+                self._capture(inputs)
+            self._check_inputs(inputs)
+            for dst, src in zip(self._buffers.inputs, inputs):
+                dst.copy_(src.reshape(-1), non_blocking=True)
+            self._module.replay(torch.cuda.current_stream(self.device).cuda_stream)
+            out = self._static_outputs
+        if self.cfg.sync_input_checks:
+            self.check_errors()
+        return out
 
     # -- capture ----------------------------------------------------------------
     def _capture(self, inputs) -> None:

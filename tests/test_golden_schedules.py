@@ -102,3 +102,24 @@ def test_published_counts_and_arenas(golden):
     assert b["bert-base|b32|s128|float16|graphs"]["plan"]["arena_bytes"] == 56631296
     assert b["bert-base|b1|s128|float32|graphs"]["plan"]["arena_bytes"] == 3539456
     assert b["gpt2-small|b1|s128|float16|graphs"]["plan"]["arena_bytes"] == 1966080
+
+
+CONFIG1 = pathlib.Path(__file__).parent / "golden" / "reference_config1.json"
+
+
+def test_config1_schedule_and_arena_match_reference():
+    """BASELINE config 1 (the FFN block, fp32, seeded 0): the reference
+    compiler's schedule -- one LayerNorm reduction with the residual add, two
+    GEMMs, the fc1 bias + tanh-GELU and the fc2 bias -- and its arena,
+    3,145,728 B (the fc1 GEMM output and the GELU output live together:
+    2 x 128 x 3072 x 4 B), written by ``dump_reference.py --config1``."""
+    from mlc.bench.workloads import make
+
+    want = json.loads(CONFIG1.read_text())
+    if want["torch"] != torch.__version__:
+        pytest.skip(f"fixture was written with torch {want['torch']}, this is {torch.__version__}")
+    model, args = make("C1", "cpu")
+    sched = build_pipeline(capture(model, args), Config())
+    _compare({"kernels": _describe(sched), "plan": _plan(sched)}, want)
+    assert sched.counts() == want["counts"] == {"extern": 2, "pointwise": 2, "reduction": 1}
+    assert sched.plan.arena_bytes == 3145728 == 2 * 128 * 3072 * 4

@@ -62,12 +62,25 @@ def test_toy_models(name, cname):
 
 
 def test_config1_ffn_block():
+    """BASELINE config 1 on the HIP path against the oracle and against the
+    reference torch backend's own output (``tests/golden/
+    reference_config1_out.npy``, written by the reference compiler): max error
+    relative to the output's largest magnitude <= 1e-5 against each."""
+    import pathlib
+
+    import numpy as np
+
     model, args = make("C1", "cpu")
     want = compile_reference(model, args)(*args)
+    fixture = pathlib.Path(__file__).parent / "golden" / "reference_config1_out.npy"
+    reference = torch.from_numpy(np.load(fixture))
     gm, ga = make("C1", "cuda")
-    got = mlc.compile(gm, ga)(*ga)
+    compiled = mlc.compile(gm, ga)
+    assert compiled.schedule.plan.arena_bytes == 3145728
+    got = compiled(*ga)
     torch.cuda.synchronize()
     assert rel_err(got, want) <= 1e-5
+    assert rel_err(got.reshape(-1), reference) <= 1e-5
 
 
 def _params_by_buffer(graph):
@@ -705,18 +718,28 @@ class _Embed(torch.nn.Module):
         return self.emb(ids) * 2.0
 
 
-@pytest.mark.parametrize("graphs", [True, False], ids=["graph", "plan"])
-def test_invalid_embedding_id_raises(graphs):
+_ID_CONFIGS = {
+    "graph": Config(),
+    "plan": Config(cuda_graphs=False),
+    "unplanned": Config(cuda_graphs=False, memory_planning=False),
+    "no_fusion": Config(elementwise_fusion=False, recompute=False, reduction_fusion=False,
+                        memory_planning=False, cuda_graphs=False),
+}
+
+
+@pytest.mark.parametrize("cname", list(_ID_CONFIGS))
+def test_invalid_embedding_id_raises(cname):
     """An id outside the table reaches only the native, bounds-checked gather
     (never torch's GPU embedding): its rows come back as zeros, and the next
     call, or ``check_errors``, raises ``ExecutionError``; after that the model
-    runs normally and matches eager PyTorch on valid ids."""
+    runs normally and matches eager PyTorch on valid ids. Held for the graph,
+    the planned run and the unplanned (per-call buffers) run."""
     from mlc.runtime.executor import ExecutionError
 
     torch.manual_seed(0)
     model = _Embed().cuda()
     ids = torch.randint(0, 1000, (2, 64), device="cuda")
-    compiled = mlc.compile(model, (ids,), Config(cuda_graphs=graphs))
+    compiled = mlc.compile(model, (ids,), _ID_CONFIGS[cname])
     kinds = [s.meta["kind"] for s in compiled._module.launch_table.values()]
     assert kinds.count("embedding") == 1 and compiled._module.flags_errors
     with torch.no_grad():
@@ -735,6 +758,26 @@ def test_invalid_embedding_id_raises(graphs):
     with pytest.raises(ExecutionError, match="outside its table"):
         compiled.check_errors()
     compiled.check_errors()
+    assert torch.equal(compiled(ids), want)
+
+
+@pytest.mark.parametrize("graphs", [True, False], ids=["graph", "plan"])
+def test_invalid_embedding_id_raises_in_the_same_call(graphs):
+    """``Config(sync_input_checks=True)``: the call that met the invalid id
+    raises ``ExecutionError`` itself; the next call runs normally."""
+    from mlc.runtime.executor import ExecutionError
+
+    torch.manual_seed(0)
+    model = _Embed().cuda()
+    ids = torch.randint(0, 1000, (2, 64), device="cuda")
+    compiled = mlc.compile(model, (ids,), Config(cuda_graphs=graphs, sync_input_checks=True))
+    with torch.no_grad():
+        want = model(ids)
+    assert torch.equal(compiled(ids), want)
+    bad = ids.clone()
+    bad[1, 3] = 5000
+    with pytest.raises(ExecutionError, match="outside its table"):
+        compiled(bad)
     assert torch.equal(compiled(ids), want)
 
 

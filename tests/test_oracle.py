@@ -84,6 +84,26 @@ def test_oracle_matches_reference_backend_outputs(golden, name, cname):
         torch.testing.assert_close(o.double(), want, rtol=2e-6, atol=1e-7)
 
 
+def test_oracle_matches_reference_backend_on_config1():
+    """BASELINE config 1 (FFN block, fp32, seeded 0): the oracle against the
+    reference torch backend's own output, written by the reference compiler
+    on this image's CPU (``tests/golden/reference_config1_out.npy``). Both
+    run the same torch CPU GEMMs and the same fp32 row statistics in the same
+    order, so they agree bit for bit."""
+    import numpy as np
+
+    from mlc.bench.workloads import make
+
+    meta = json.loads((GOLDEN.parent / "reference_config1.json").read_text())
+    if meta["torch"] != torch.__version__:
+        pytest.skip(f"fixture was written with torch {meta['torch']}")
+    want = torch.from_numpy(np.load(GOLDEN.parent / "reference_config1_out.npy"))
+    model, args = make("C1", "cpu")
+    got = compile_reference(model, args)(*args)
+    assert list(got.shape) == meta["output_shape"]
+    torch.testing.assert_close(got.reshape(-1), want, rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("name", [m[0] for m in all_models()])
 def test_exactness_classes_are_bit_identical(name):
     """Configs without reduction fusion evaluate the same ops in the same
