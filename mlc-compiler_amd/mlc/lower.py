@@ -29,7 +29,7 @@ from __future__ import annotations
 from .codegen.index import IndexMap, flat_index
 from .config import Config
 from .ir.graph import Graph, Node, Value
-from .ir.ops import _S, lookup
+from .ir.ops import _literal, lookup
 from .ir.scalar import Const, Expr, Load, Ref, loads, substitute
 from .kernels import ExternKernel, KernelArg, PointwiseKernel, Schedule
 from .passes.fusion import BROADCAST, FULL, KernelGroup, _fits_space, group_space
@@ -165,7 +165,7 @@ class KernelAssembler:
     def literal_or_passthrough(a):
         """Non-tensor arguments: numbers become literals; dims, dtypes and the
         like pass through for the lowering rule to read."""
-        return _S(a) if isinstance(a, (bool, int, float)) else a
+        return _literal(a) if isinstance(a, (bool, int, float)) else a
 
     def compact(self, exprs: list[Expr]) -> tuple[list[KernelArg], dict[Expr, Expr] | None]:
         """Drop slots none of ``exprs`` reads: the kept operands, and the
