@@ -1,7 +1,8 @@
 """Benchmark: BERT-base fp16 s128 ms/forward (b1 and b32) through hipGraph
 replay, and the fused kernels' HBM bandwidth against the MI355X peak.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-variants]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-cpu-c5]
+                    [--no-variants]
 
 One step is one forward of the compiled model (one hipGraph replay: every
 generated kernel plus every extern library call) over inputs already resident
@@ -16,9 +17,20 @@ whose launches are 4-30x larger). Beside each kernel figure,
 ``copy_ceiling`` times a plain packed copy kernel of the same algorithmic
 bytes the same way: the practical ceiling once each launch's fixed cost is
 counted.
+The per-kernel loop launches a kernel back to back on the same buffers, so
+after the first launch its inputs come from the 256 MB Infinity Cache (MALL).
+Two more b32 figures price the kernels where they run: ``fused_b32_in_forward``
+decomposes the forward's hipGraph (the generated kernels' excess over empty
+graph nodes, and their cost with their launches, against the library GEMMs
+alone; ``mlc.bench.launch_floor``), and ``fused_b32_cold`` launches every
+generated function once right after a 1 GiB fill that evicts the L2s and the
+MALL (inputs from HBM; ``mlc.bench.cold``), beside a plain copy of the same
+bytes launched the same way. ``roofline.in_forward`` and ``roofline.cold``
+give the dominant kernel's figures the same two ways.
 ``schedule_variants`` times the opt-in schedule changes (never the headline
 value). The CPU baseline is the oracle (the kernel IR executed with torch on
-the host) on a bounded number of b1 forwards. Prints one JSON line.
+the host) on a bounded number of forwards of every config. Prints one JSON
+line.
 """
 
 from __future__ import annotations
@@ -123,9 +135,26 @@ def _kernel_table(compiled, iters: int):
         replayed = i
         bound = payload.bound if native else payload
         ms = rt.time_bound(bound, iters, stream)
-        rows.append((k, rt.launch_table[k.name].symbol, algorithmic_bytes(k), ms))
+        rows.append((k, rt.launch_table[k.name].symbol, algorithmic_bytes(k), ms, bound))
     torch.cuda.synchronize()
     return rows
+
+
+def _per_symbol(rows) -> dict:
+    per_symbol = {}
+    for k, sym, nbytes, ms, _ in rows:
+        agg = per_symbol.setdefault(sym, {"total_bytes": 0, "bytes": nbytes, "launch_ms": [],
+                                          "kernel": k})
+        agg["total_bytes"] += nbytes
+        agg["launch_ms"].append(ms)
+    return per_symbol
+
+
+def _dominant(rows) -> str:
+    """The generated function moving the most algorithmic bytes per forward
+    (a property of the schedule, not of one timing run)."""
+    per_symbol = _per_symbol(rows)
+    return max(per_symbol, key=lambda s: per_symbol[s]["total_bytes"])
 
 
 def _fused_aggregate(rows, iters: int) -> dict:
@@ -143,6 +172,78 @@ def _fused_aggregate(rows, iters: int) -> dict:
     return {"kernels": len(rows), "algorithmic_bytes": fused_bytes, "ms": round(fused_ms, 4),
             "achieved": round(fused_gbs, 1), "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
             "copy_ceiling_ms": round(copy_ms, 4), "kernels_vs_copy": round(copy_ms / fused_ms, 4)}
+
+
+def _in_forward(compiled, inputs, rows, dom_sym: str, replays: int) -> dict:
+    """What the generated kernels cost inside the b32 forward (hipGraph
+    replays through ``mlc.bench.launch_floor``): the forward against the same
+    graph with every generated kernel an empty node (their excess over an
+    empty node) and against the library calls alone (their cost with their
+    launches); the dominant function's own excess per launch the same way."""
+    from mlc.bench.launch_floor import decompose_compiled
+    from mlc.bench.roofline import HBM_PEAK_GBS
+
+    d = decompose_compiled(compiled, inputs, replays, families=[dom_sym], shapes=False,
+                           log=lambda line: print(f"# {line}", file=sys.stderr, flush=True))
+    fused_bytes = sum(r[2] for r in rows)
+
+    def rate(ms):
+        gbs = fused_bytes / (ms * 1e-3) / 1e9
+        return round(ms, 4), round(gbs, 1), round(gbs / HBM_PEAK_GBS, 4)
+
+    excess = rate(d["full"] - d["base"])
+    with_launch = rate(d["full"] - d["library_only"])
+    fam, n, fam_ms = d["families"][0]
+    nbytes = next(r[2] for r in rows if r[1] == dom_sym)
+    per_launch_us = fam_ms * 1e3 / n
+    gbs = nbytes / per_launch_us / 1e3
+    return {
+        "forward_ms": round(d["full"], 4), "library_calls_only_ms": round(d["library_only"], 4),
+        "library_calls_plus_empty_ms": round(d["base"], 4), "generated_kernels": d["generated"],
+        "algorithmic_bytes": fused_bytes,
+        "excess_over_empty_nodes": dict(zip(("ms", "achieved", "frac"), excess)),
+        "with_launches": dict(zip(("ms", "achieved", "frac"), with_launch)),
+        "dominant": {"symbol": fam, "launches": n, "excess_us_per_launch": round(per_launch_us, 3),
+                     "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)},
+        "replays": replays}
+
+
+def _cold(compiled, rows) -> dict:
+    """Every generated function of one forward launched once right after a
+    1 GiB fill (L2s and the 256 MB MALL evicted: inputs from HBM), and a
+    plain copy of the same bytes the same way (``mlc.bench.cold``)."""
+    import torch
+
+    from mlc.bench.cold import cold_launch_us
+    from mlc.bench.roofline import HBM_PEAK_GBS
+
+    rt = compiled._module
+    per_symbol = {}
+    for r in rows:
+        per_symbol.setdefault(r[1], (r[2], r[4], []))[2].append(r)
+    global _CEILING
+    if _CEILING is None:
+        _copy_period_us(1 << 20, 2)
+    families = {}
+    for sym, (nbytes, bound, launches) in per_symbol.items():
+        if bound.grid == 0:
+            continue
+        us = cold_launch_us(lambda b=bound: rt.run_bound(b))
+        copy = _CEILING.launcher(nbytes)
+        copy_us = cold_launch_us(copy)
+        families[sym] = {"launches": len(launches), "bytes_per_launch": nbytes,
+                         "cold_us": round(us, 3), "copy_cold_us": round(copy_us, 3),
+                         "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del copy
+    torch.cuda.synchronize()
+    total_bytes = sum(f["bytes_per_launch"] * f["launches"] for f in families.values())
+    total_us = sum(f["cold_us"] * f["launches"] for f in families.values())
+    copy_us = sum(f["copy_cold_us"] * f["launches"] for f in families.values())
+    gbs = total_bytes / total_us / 1e3
+    return {"families": families, "algorithmic_bytes": total_bytes,
+            "ms": round(total_us / 1e3, 4), "achieved": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "copy_ceiling_ms": round(copy_us / 1e3, 4),
+            "kernels_vs_copy": round(copy_us / total_us, 4)}
 
 
 def _attention_row(compiled, iters: int) -> dict:
@@ -200,13 +301,16 @@ def _time_cpu(fn, args, warmup: int, min_runs: int, budget_s: float):
     return statistics.median(times), times, out
 
 
-def _cpu_baseline(hip_outputs: dict, budget_s: float):
+def _cpu_baseline(hip_outputs: dict, budget_s: float, with_c5: bool = True):
     """The CPU oracle (the kernel IR executed with torch on the host, fp32
     math, fp16 storage; its own CPU GEMMs) timed on the host's cores for
-    configs 2 (the headline), 1 and 4, 2 warm-ups then the median of the
-    timed forwards (``mlc/bench/runner.py:106-110``). Its outputs double as
-    the parity check of the GPU results timed above (``hip_outputs``): max
-    error relative to the oracle output's largest magnitude."""
+    every BASELINE config: 2 (the headline), 1, 3 and 4 with 2 warm-ups (1
+    for config 4) then the median of the timed forwards
+    (``mlc/bench/runner.py:106-110``); config 5 (GPT-2 b32 s512, about 30 s
+    per forward on 16 threads) as one forward with no warm-up. Its outputs
+    double as the parity check of the GPU results timed above
+    (``hip_outputs``): max error relative to the oracle output's largest
+    magnitude."""
     import torch
 
     from mlc.bench.workloads import make
@@ -216,8 +320,10 @@ def _cpu_baseline(hip_outputs: dict, budget_s: float):
     torch.set_num_threads(threads)
     timed = {}
     parity = {}
-    for key, warmup, min_runs, budget in (("C2", 2, 5, budget_s), ("C1", 2, 5, 2.0),
-                                          ("C4", 1, 3, 0.0)):
+    plan = [("C2", 2, 5, budget_s), ("C1", 2, 5, 2.0), ("C3", 2, 5, 2.0), ("C4", 1, 3, 0.0)]
+    if with_c5:
+        plan.append(("C5", 0, 1, 0.0))
+    for key, warmup, min_runs, budget in plan:
         model, args = make(key, "cpu")
         ref = compile_reference(model, args)
         med, times, out = _time_cpu(ref, args, warmup, min_runs, budget)
@@ -238,8 +344,9 @@ def _cpu_baseline(hip_outputs: dict, budget_s: float):
                    f"BASELINE config 2, BERT-base fp16 b1 s128: median of {len(times)} forwards "
                    f"after 2 warm-ups, {sum(times):.1f}s of CPU work, os.cpu_count()={threads}"),
         "other_configs_ms_per_forward": {
-            key: {"median_ms": round(timed[key][0] * 1e3, 3), "runs": len(timed[key][1])}
-            for key in ("C1", "C4")},
+            key: {"median_ms": round(timed[key][0] * 1e3, 3), "runs": len(timed[key][1]),
+                  "warmup": next(w for k, w, _, _ in plan if k == key)}
+            for key in timed if key != "C2"},
     }, parity
 
 
@@ -250,7 +357,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--kernel-iters", type=int, default=50)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--floor-replays", type=int, default=100,
+                    help="graph replays per decomposition graph of the b32 in-forward figure")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-c5", action="store_true",
+                    help="leave config 5 (one ~30 s CPU forward) out of the CPU baseline")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the schedule variants (the reference schedule only)")
     opts = ap.parse_args()
@@ -283,7 +394,11 @@ def main() -> int:
         results[key]["arena_bytes"] = compiled.schedule.arena_bytes
         results[key]["forward_bytes"] = forward_bytes(compiled.schedule)
         if key == "C4":
-            tables[key] = _kernel_table(compiled, opts.kernel_iters)
+            rows = tables[key] = _kernel_table(compiled, opts.kernel_iters)
+            results[key]["dominant"] = _dominant(rows)
+            results[key]["in_forward"] = _in_forward(compiled, inputs, rows,
+                                                     results[key]["dominant"], opts.floor_replays)
+            results[key]["cold"] = _cold(compiled, rows)
         print(f"# {key}: {results[key]}", file=sys.stderr, flush=True)
         del compiled, model, inputs
         torch.cuda.empty_cache()
@@ -330,17 +445,12 @@ def main() -> int:
         del compiled, model, inputs
         torch.cuda.empty_cache()
 
-    # dominant fused kernel at b32: the function moving the most algorithmic
-    # bytes per forward (a property of the schedule, not of one timing run)
     rows = tables["C4"]
-    per_symbol = {}
-    for k, sym, nbytes, ms in rows:
-        agg = per_symbol.setdefault(sym, {"total_bytes": 0, "bytes": nbytes, "launch_ms": [],
-                                          "kernel": k})
-        agg["total_bytes"] += nbytes
-        agg["launch_ms"].append(ms)
-    dom_sym = max(per_symbol, key=lambda s: per_symbol[s]["total_bytes"])
+    per_symbol = _per_symbol(rows)
+    dom_sym = results["C4"]["dominant"]
     dom = per_symbol[dom_sym]
+    in_forward = results["C4"]["in_forward"]
+    cold = results["C4"]["cold"]
     launch_ms = statistics.mean(dom["launch_ms"])
     achieved = dom["bytes"] / (launch_ms * 1e-3) / 1e9
 
@@ -389,13 +499,25 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _measured_traffic(dom_sym),
             "copy_ceiling": _copy_ceiling(dom["bytes"], launch_ms * 1e3, opts.kernel_iters),
+            # the same function inside the forward (its excess over an empty
+            # graph node) and launched once with the caches cold
+            "in_forward": in_forward["dominant"],
+            "cold": {"launch_us": cold["families"][dom_sym]["cold_us"],
+                     "copy_cold_us": cold["families"][dom_sym]["copy_cold_us"],
+                     "frac": cold["families"][dom_sym]["frac"]},
         },
+        # every generated kernel of the b32 forward, three ways: back-to-back
+        # launches (inputs MALL-resident after the first), inside the forward,
+        # and each launch after a cache-evicting fill
         "fused_b32": _fused_aggregate(rows, opts.kernel_iters),
+        "fused_b32_in_forward": {k: v for k, v in in_forward.items() if k != "dominant"},
+        "fused_b32_cold": {k: v for k, v in cold.items() if k != "families"},
         "cpu_baseline": None,
         "parity": None,
     }
     if not opts.no_cpu_baseline:
-        line["cpu_baseline"], checked = _cpu_baseline(outputs, opts.cpu_budget)
+        line["cpu_baseline"], checked = _cpu_baseline(outputs, opts.cpu_budget,
+                                                      with_c5=not opts.no_cpu_c5)
         # BERT's pooled output is the one output held to 3e-3 instead of the
         # north-star 2e-3: fp16 rounding flips saturate the 12-layer hidden
         # state, and the oracle is as far from itself across devices

@@ -96,16 +96,31 @@ def decompose(workload: str, replays: int = 200, blas: str | None = None):
     import mlc
     from mlc.bench.workloads import make
     from mlc.config import Config
-    from mlc.runtime import native
-    from mlc.runtime.hip_runtime import Bound
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     if blas:
         torch.backends.cuda.preferred_blas_library(blas)
-    lib = native.load_library()
     model, inputs = make(workload, device)
     compiled = mlc.compile(model, inputs, Config())
+    d = decompose_compiled(compiled, inputs, replays)
+    d.update(workload=workload, blas=blas)
+    return d
+
+
+def decompose_compiled(compiled, inputs, replays: int = 200, families=None, shapes: bool = True,
+                       log=print):
+    """The graphs above for an already compiled model (``families``: the
+    generated functions to time one by one, every one when None; ``shapes``:
+    also the all-empty graphs; ``log``: where progress lines go)."""
+    import torch
+
+    from mlc.runtime import native
+    from mlc.runtime.hip_runtime import Bound
+
+    index = compiled.device.index
+    device = torch.device("cuda", torch.cuda.current_device() if index is None else index)
+    lib = native.load_library()
     compiled(*inputs)
     torch.cuda.synchronize()
     rt = compiled._module
@@ -168,7 +183,7 @@ def decompose(workload: str, replays: int = 200, blas: str | None = None):
     t1.record()
     t1.synchronize()
     executor_ms = t0.elapsed_time(t1) / replays
-    print(f"executor graph replay: {executor_ms * 1e3:.1f} us per forward", flush=True)
+    log(f"executor graph replay: {executor_ms * 1e3:.1f} us per forward")
 
     stream = torch.cuda.Stream(device)
     results = []
@@ -181,21 +196,24 @@ def decompose(workload: str, replays: int = 200, blas: str | None = None):
             results.append((label, g.nodes(), ms, note))
         finally:
             g.close()
-        print(f"{label}: {results[-1][1]} nodes, {ms * 1e3:.1f} us per replay", flush=True)
+        log(f"{label}: {results[-1][1]} nodes, {ms * 1e3:.1f} us per replay")
         return ms
 
     n = len(entries)
-    measure(f"empty x {n}", lambda s: [launch_empty(s) for _ in range(n)])
-    measure(f"empty x {n}, real grids", body(lambda f: False, real_lib=False, real_grids=True))
+    if shapes:
+        measure(f"empty x {n}", lambda s: [launch_empty(s) for _ in range(n)])
+        measure(f"empty x {n}, real grids", body(lambda f: False, real_lib=False, real_grids=True))
     base = measure(f"library calls ({n_lib}) + empty ({n_gen})", body(lambda f: False))
-    measure(f"library calls only ({n_lib})", body(lambda f: False, empty_for_gen=False))
+    library = measure(f"library calls only ({n_lib})", body(lambda f: False, empty_for_gen=False))
     full = measure("forward (every node real)", body(lambda f: True))
-    families = {}
+    launches_of = {}
     for kind, p, fam in entries:
         if kind == "gen":
-            families.setdefault(fam, []).append(p)
+            launches_of.setdefault(fam, []).append(p)
     fam_rows = []
-    for fam, launches in families.items():
+    for fam, launches in launches_of.items():
+        if families is not None and fam not in families:
+            continue
         ms = measure(f"family {fam} real", body(lambda f, fam=fam: f == fam))
         fam_rows.append((fam, len(launches), ms - base))
     torch.cuda.synchronize()
@@ -207,8 +225,8 @@ def decompose(workload: str, replays: int = 200, blas: str | None = None):
         spec = rt.launch_table.get(k.name)
         if spec is not None and spec.symbol not in summaries:
             summaries[spec.symbol] = k.summary().split(": ", 1)[-1][:60]
-    return {"workload": workload, "blas": blas, "entries": n, "generated": n_gen, "library": n_lib,
-            "results": results, "families": fam_rows, "base": base, "full": full,
+    return {"entries": n, "generated": n_gen, "library": n_lib, "results": results,
+            "families": fam_rows, "base": base, "library_only": library, "full": full,
             "executor": executor_ms, "summaries": summaries, "replays": replays}
 
 

@@ -535,19 +535,16 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
     in_types = [compute_type(a.dtype) for a in k.inputs]
     temp_types: dict[str, str] = {}
     packs = -(-N // V)
-    B, U = pointwise_geometry(packs)
+    exact = N % V == 0
+    B = pointwise_geometry(packs)
     L: list[str] = []
     L.append(f"extern \"C\" __global__ void __launch_bounds__({B}) "
              f"KERNEL({', '.join(_params(k))}) {{")
-    L.append(f"  // pointwise over {list(k.space)} = {N} elements, {V}-element packs, "
-             f"{U} per thread")
+    L.append(f"  // pointwise over {list(k.space)} = {N} elements, one {V}-element pack "
+             "per thread")
     L.append(f"  constexpr {it} N = ({it}){N};")
     L.append(f"  constexpr int V = {V};")
-    L.append(f"  const {it} base = ({it})blockIdx.x * {B * U} + threadIdx.x;")
-    L.append("#pragma unroll")
-    L.append(f"  for (int u = 0; u < {U}; ++u) {{")
-    L.append(f"  const {it} e0 = (base + ({it})u * {B}) * V;")
-    L.append("  if (e0 >= N) break;")
+    L.append(f"  const {it} base = ({it})blockIdx.x * {B} + threadIdx.x;")
 
     half_slots = half_inputs(k)
     defs = dict(k.body)
@@ -562,47 +559,54 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
             lines.append(f"{indent}const {t} {name} = {code};")
         return lines, r
 
-    # -- vector path --
-    vec: list[str] = []
-    for i, (a, acc) in enumerate(zip(k.inputs, accesses)):
-        ct = in_types[i]
-        if acc.mode == "uniform":
-            vec.append(f"    const {ct} v{i} = mlc::ld(in{i} + {offset(a, 'e0')});")
-        elif acc.mode == "affine" and acc.aligned:
-            vec.append(f"    {ct} v{i}[V]; mlc::load_pack<V>(v{i}, in{i} + {offset(a, 'e0')});")
-        elif acc.mode == "affine":
-            vec.append(f"    {ct} v{i}[V];")
-            vec.append(f"    {{ const {it} o = {offset(a, 'e0')};")
-            vec.append("#pragma unroll")
-            vec.append(f"      for (int j = 0; j < V; ++j) v{i}[j] = mlc::ld(in{i} + o + ({it})j * ({it}){acc.stride}); }}")
-        else:
-            vec.append(f"    {ct} v{i}[V];")
-            vec.append("#pragma unroll")
-            vec.append(f"    for (int j = 0; j < V; ++j) v{i}[j] = mlc::ld(in{i} + {offset(a, '(e0 + (' + it + ')j)')});")
+    # -- vector path: the pack's loads, then its arithmetic and stores --
+    def pack_loads(e0: str, sfx: str) -> list[str]:
+        out = []
+        for i, (a, acc) in enumerate(zip(k.inputs, accesses)):
+            ct, v = in_types[i], f"v{i}{sfx}"
+            if acc.mode == "uniform":
+                out.append(f"    const {ct} {v} = mlc::ld(in{i} + {offset(a, e0)});")
+            elif acc.mode == "affine" and acc.aligned:
+                out.append(f"    {ct} {v}[V]; mlc::load_pack<V>({v}, in{i} + {offset(a, e0)});")
+            elif acc.mode == "affine":
+                out.append(f"    {ct} {v}[V];")
+                out.append(f"    {{ const {it} o = {offset(a, e0)};")
+                out.append("#pragma unroll")
+                out.append(f"      for (int j = 0; j < V; ++j) {v}[j] = mlc::ld(in{i} + o + ({it})j * ({it}){acc.stride}); }}")
+            else:
+                out.append(f"    {ct} {v}[V];")
+                out.append("#pragma unroll")
+                out.append(f"    for (int j = 0; j < V; ++j) {v}[j] = mlc::ld(in{i} + {offset(a, '(' + e0 + ' + (' + it + ')j)')});")
+        return out
 
-    def ref_vec(slot):
-        mode = accesses[slot].mode
-        return (f"v{slot}" if mode == "uniform" else f"v{slot}[j]"), in_types[slot]
+    def pack_compute_store(e0: str, sfx: str) -> list[str]:
+        def ref_vec(slot):
+            mode = accesses[slot].mode
+            return (f"v{slot}{sfx}" if mode == "uniform" else f"v{slot}{sfx}[j]"), in_types[slot]
 
-    out_vals = []
-    for i, a in enumerate(k.outputs):
-        vec.append(f"    {compute_type_of_out(k, a)} o{i}[V];")
-    vec.append("#pragma unroll")
-    vec.append("    for (int j = 0; j < V; ++j) {")
-    blines, r = body_lines(ref_vec, "      ")
-    vec += blines
-    for i, a in enumerate(k.outputs):
-        code, _ = r.store(k.out_expr[a.value.name], a.dtype == torch.float16)
-        vec.append(f"      o{i}[j] = {code};")
-    vec.append("    }")
-    for i, (a, acc) in enumerate(zip(k.outputs, out_access)):
-        if acc.mode == "affine" and acc.aligned:
-            vec.append(f"    mlc::store_pack<V>(out{i} + {offset(a, 'e0')}, o{i});")
-        else:
-            vec.append("#pragma unroll")
-            vec.append(f"    for (int j = 0; j < V; ++j) mlc::st(out{i} + {offset(a, '(e0 + (' + it + ')j)')}, o{i}[j]);")
+        out = []
+        for i, a in enumerate(k.outputs):
+            out.append(f"    {compute_type_of_out(k, a)} o{i}[V];")
+        out.append("#pragma unroll")
+        out.append("    for (int j = 0; j < V; ++j) {")
+        blines, r = body_lines(ref_vec, "      ")
+        out += blines
+        for i, a in enumerate(k.outputs):
+            code, _ = r.store(k.out_expr[a.value.name], a.dtype == torch.float16)
+            out.append(f"      o{i}[j] = {code};")
+        out.append("    }")
+        for i, (a, acc) in enumerate(zip(k.outputs, out_access)):
+            if acc.mode == "affine" and acc.aligned:
+                out.append(f"    mlc::store_pack<V>(out{i} + {offset(a, e0)}, o{i});")
+            else:
+                out.append("#pragma unroll")
+                out.append(f"    for (int j = 0; j < V; ++j) mlc::st(out{i} + {offset(a, '(' + e0 + ' + (' + it + ')j)')}, o{i}[j]);")
+        return out
 
-    exact = N % V == 0
+    L.append(f"  const {it} e0 = base * V;")
+    L.append("  if (e0 >= N) return;")
+    vec = pack_loads("e0", "") + pack_compute_store("e0", "")
+
     if exact:
         L.append("  {")
         L += vec
@@ -622,12 +626,11 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
             L.append(f"      mlc::st(out{i} + {offset(a, 'e')}, {code});")
         L.append("    }")
         L.append("  }")
-    L.append("  }")
     L.append("}")
 
-    grid = max(1, -(-packs // (B * U)))
+    grid = max(1, -(-packs // B))
     spec = LaunchSpec("", grid, B, 0,
-                      {"kind": "pointwise", "vec": V, "numel": N, "unroll": U,
+                      {"kind": "pointwise", "vec": V, "numel": N,
                        "access": [a.mode + ("+aligned" if a.aligned else "") for a in accesses]})
     return "\n".join(L), spec
 
@@ -770,15 +773,15 @@ def emit_transpose(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
     return "\n".join(L), spec
 
 
-#: pointwise launch shape: threads per workgroup, and packs per thread once
-#: a launch has more than ``unroll_above`` packs
-POINTWISE_TUNING = {"block": 512, "unroll": 1, "unroll_above": 1 << 30}
+#: pointwise launch shape: threads per workgroup (one pack per thread: more
+#: packs per thread, with every pack's loads issued first, measured slower at
+#: every BERT b32 size, MALL-resident or cold)
+POINTWISE_TUNING = {"block": 512}
 
 
-def pointwise_geometry(packs: int) -> tuple[int, int]:
-    t = POINTWISE_TUNING
-    u = t["unroll"] if packs > t["unroll_above"] else 1
-    return t["block"], u
+def pointwise_geometry(packs: int) -> int:
+    """Threads per workgroup of a pointwise launch over ``packs`` packs."""
+    return POINTWISE_TUNING["block"]
 
 
 def compute_type_of_out(k, a) -> str:
