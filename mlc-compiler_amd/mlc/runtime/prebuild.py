@@ -39,6 +39,10 @@ DEFAULT = [("C1", Config()), ("C2", Config()), ("C3", Config()), ("C4", Config()
            ("C2", FAST), ("C4", FAST), ("C2", ATTENTION), ("C3", ATTENTION),
            ("C4", ATTENTION), ("C5", ATTENTION), ("C2", ALL), ("C3", ALL), ("C4", ALL),
            ("C5", ALL)]
+# the planned / unplanned pairs the exactness tests compile (the unplanned
+# schedule is the planned one, so each pair shares its code object)
+DEFAULT += [(key, cfg) for key in ("C2", "C3", "C4")
+            for cfg in (Config(reduction_fusion=False, cuda_graphs=False), Config(cuda_graphs=False))]
 
 
 def prebuild(items=None, verbose: bool = True) -> None:

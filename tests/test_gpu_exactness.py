@@ -14,8 +14,8 @@ configurations (``tests/test_correctness.py:51-74`` and
   so fusing or recomputing a chain must not move a bit.
 * planned = unplanned: the arena only moves buffers, so the results are
   bit-identical. Held here for the toy models under the reference's planned /
-  unplanned pair and under all passes, and for BERT-base fp16 b1 (BASELINE
-  config 2).
+  unplanned pair and under all passes, and for BASELINE configs 2-4 (BERT-base
+  fp16 b1 and b32, GPT-2 small fp16 b1).
 
 Every comparison is at rtol = atol = 0.
 """
@@ -102,22 +102,26 @@ def test_planning_does_not_change_hip_results(name, pair):
 
 
 @pytest.mark.parametrize("pair", list(PLANNING_PAIRS))
-def test_planning_does_not_change_bert_fp16_results(pair):
-    """BASELINE config 2 (BERT-base fp16 b1 s128): the arena moves buffers
-    only, so the pooled output is bit-identical with and without it."""
-    model, args = make("C2", "cuda")
-    print(f"planned vs unplanned: C2 ({pair})", flush=True)
+@pytest.mark.parametrize("key", ["C2", "C3", "C4"])
+def test_planning_does_not_change_fp16_model_results(key, pair):
+    """BASELINE configs 2-4 (BERT-base fp16 b1 and b32, GPT-2 small fp16
+    b1): the arena moves buffers only, so the outputs are bit-identical with
+    and without it."""
+    model, args = make(key, "cuda")
+    print(f"planned vs unplanned: {key} ({pair})", flush=True)
     planned, unplanned = PLANNING_PAIRS[pair]
     _assert_bit_identical(_run(model, args, planned), _run(model, args, unplanned),
-                          f"C2: planned vs unplanned ({pair})")
+                          f"{key}: planned vs unplanned ({pair})")
 
 
-def test_graph_replay_equals_planned_run_bert_fp16():
-    """The captured hipGraph replays exactly the planned run (config 2)."""
-    model, args = make("C2", "cuda")
+@pytest.mark.parametrize("key", ["C2", "C3", "C4"])
+def test_graph_replay_equals_planned_run_fp16(key):
+    """The captured hipGraph replays exactly the planned run, on every replay."""
+    model, args = make(key, "cuda")
+    print(f"graph replay vs planned run: {key}", flush=True)
     eager = _run(model, args, Config(cuda_graphs=False))
     compiled = mlc.compile(model, args, Config())
     for _ in range(3):
         got = [o.detach().cpu().clone() for o in flat_outputs(compiled(*args))]
         torch.cuda.synchronize()
-        _assert_bit_identical(got, eager, "C2: graph replay vs planned run")
+        _assert_bit_identical(got, eager, f"{key}: graph replay vs planned run")
