@@ -18,15 +18,12 @@ whose launches are 4-30x larger). Beside each kernel figure,
 bytes the same way: the practical ceiling once each launch's fixed cost is
 counted.
 The per-kernel loop launches a kernel back to back on the same buffers, so
-after the first launch its inputs come from the 256 MB Infinity Cache (MALL).
-Two more b32 figures price the kernels where they run: ``fused_b32_in_forward``
-decomposes the forward's hipGraph (the generated kernels' excess over empty
+after the first launch its inputs are cache-resident (the 256 MB Infinity
+Cache holds them). ``fused_b32_in_forward`` prices the kernels where they run:
+it decomposes the forward's hipGraph (the generated kernels' excess over empty
 graph nodes, and their cost with their launches, against the library GEMMs
-alone; ``mlc.bench.launch_floor``), and ``fused_b32_cold`` launches every
-generated function once right after a 1 GiB fill that evicts the L2s and the
-MALL (inputs from HBM; ``mlc.bench.cold``), beside a plain copy of the same
-bytes launched the same way. ``roofline.in_forward`` and ``roofline.cold``
-give the dominant kernel's figures the same two ways.
+alone; ``mlc.bench.launch_floor``), and ``roofline.in_forward`` gives the
+dominant kernel's excess per launch the same way.
 ``schedule_variants`` times the opt-in schedule changes (never the headline
 value). The CPU baseline is the oracle (the kernel IR executed with torch on
 the host) on a bounded number of forwards of every config. Prints one JSON
@@ -208,44 +205,6 @@ def _in_forward(compiled, inputs, rows, dom_sym: str, replays: int) -> dict:
         "replays": replays}
 
 
-def _cold(compiled, rows) -> dict:
-    """Every generated function of one forward launched once right after a
-    1 GiB fill (L2s and the 256 MB MALL evicted: inputs from HBM), and a
-    plain copy of the same bytes the same way (``mlc.bench.cold``)."""
-    import torch
-
-    from mlc.bench.cold import cold_launch_us
-    from mlc.bench.roofline import HBM_PEAK_GBS
-
-    rt = compiled._module
-    per_symbol = {}
-    for r in rows:
-        per_symbol.setdefault(r[1], (r[2], r[4], []))[2].append(r)
-    global _CEILING
-    if _CEILING is None:
-        _copy_period_us(1 << 20, 2)
-    families = {}
-    for sym, (nbytes, bound, launches) in per_symbol.items():
-        if bound.grid == 0:
-            continue
-        us = cold_launch_us(lambda b=bound: rt.run_bound(b))
-        copy = _CEILING.launcher(nbytes)
-        copy_us = cold_launch_us(copy)
-        families[sym] = {"launches": len(launches), "bytes_per_launch": nbytes,
-                         "cold_us": round(us, 3), "copy_cold_us": round(copy_us, 3),
-                         "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
-        del copy
-    torch.cuda.synchronize()
-    total_bytes = sum(f["bytes_per_launch"] * f["launches"] for f in families.values())
-    total_us = sum(f["cold_us"] * f["launches"] for f in families.values())
-    copy_us = sum(f["copy_cold_us"] * f["launches"] for f in families.values())
-    gbs = total_bytes / total_us / 1e3
-    return {"families": families, "algorithmic_bytes": total_bytes,
-            "ms": round(total_us / 1e3, 4), "achieved": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "copy_ceiling_ms": round(copy_us / 1e3, 4),
-            "kernels_vs_copy": round(copy_us / total_us, 4)}
-
-
 def _attention_row(compiled, iters: int) -> dict:
     """Average launch time and algorithmic bandwidth of the fused attention
     kernel (every layer shares one function)."""
@@ -398,7 +357,6 @@ def main() -> int:
             results[key]["dominant"] = _dominant(rows)
             results[key]["in_forward"] = _in_forward(compiled, inputs, rows,
                                                      results[key]["dominant"], opts.floor_replays)
-            results[key]["cold"] = _cold(compiled, rows)
         print(f"# {key}: {results[key]}", file=sys.stderr, flush=True)
         del compiled, model, inputs
         torch.cuda.empty_cache()
@@ -450,7 +408,6 @@ def main() -> int:
     dom_sym = results["C4"]["dominant"]
     dom = per_symbol[dom_sym]
     in_forward = results["C4"]["in_forward"]
-    cold = results["C4"]["cold"]
     launch_ms = statistics.mean(dom["launch_ms"])
     achieved = dom["bytes"] / (launch_ms * 1e-3) / 1e9
 
@@ -499,19 +456,14 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _measured_traffic(dom_sym),
             "copy_ceiling": _copy_ceiling(dom["bytes"], launch_ms * 1e3, opts.kernel_iters),
-            # the same function inside the forward (its excess over an empty
-            # graph node) and launched once with the caches cold
+            # the same function inside the forward: its excess over an empty
+            # graph node
             "in_forward": in_forward["dominant"],
-            "cold": {"launch_us": cold["families"][dom_sym]["cold_us"],
-                     "copy_cold_us": cold["families"][dom_sym]["copy_cold_us"],
-                     "frac": cold["families"][dom_sym]["frac"]},
         },
-        # every generated kernel of the b32 forward, three ways: back-to-back
-        # launches (inputs MALL-resident after the first), inside the forward,
-        # and each launch after a cache-evicting fill
+        # every generated kernel of the b32 forward, two ways: back-to-back
+        # launches on the same buffers, and inside the forward
         "fused_b32": _fused_aggregate(rows, opts.kernel_iters),
         "fused_b32_in_forward": {k: v for k, v in in_forward.items() if k != "dominant"},
-        "fused_b32_cold": {k: v for k, v in cold.items() if k != "families"},
         "cpu_baseline": None,
         "parity": None,
     }

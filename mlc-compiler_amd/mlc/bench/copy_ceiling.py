@@ -77,25 +77,6 @@ class CopyCeiling:
         self._cache[nbytes] = float(ms.value) * 1e3
         return self._cache[nbytes]
 
-    def launcher(self, nbytes: int):
-        """A callable launching one copy of ``nbytes`` (half read, half
-        written) on torch's current stream; it holds its buffers."""
-        import torch
-
-        packs = max(1, nbytes // 32)
-        src = torch.ones(packs * 8, dtype=torch.float16, device="cuda")
-        dst = torch.empty_like(src)
-        args = struct.pack("<QQI", src.data_ptr(), dst.data_ptr(), packs)
-        grid = -(-packs // BLOCK)
-
-        def launch() -> None:
-            stream = torch.cuda.current_stream().cuda_stream
-            native.check(self.lib.mlc_launch(self._fn, grid, BLOCK, 0, args, len(args), stream),
-                         "mlc_launch(mlc_copy_ceiling)")
-
-        launch.buffers = (src, dst)
-        return launch
-
     def close(self) -> None:
         if self._ctx:
             self.lib.mlc_ctx_destroy(self._ctx)

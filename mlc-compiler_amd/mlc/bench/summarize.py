@@ -18,7 +18,7 @@ reads for its ``traffic`` field.
 ``stats``: a kernel trace (``--kernel-trace --stats``) of ``bench.py``: the top
 of rocprofv3's own per-kernel table, then every generated function of BERT
 b32 with its dispatches split by what ran just before (``trace_split``: the
-timing loop, after the cache-evicting fill, in sequence as in a forward).
+timing loop, or in sequence as in a forward).
 
 Symbols are matched to kernels by compiling the workload's schedule on the CPU
 (the symbol is a hash of the generated function's body).
@@ -187,11 +187,10 @@ def stats(opts) -> str:
     split = {s: v for s, v in classify(trace).items() if s in info}
     L += ["", "Generated functions of the BERT b32 reference schedule, their dispatches split by "
           "what ran just before each (`trace_split.py`): `loop`, the same kernel (the timing "
-          "loop: inputs resident in the 256 MB MALL after the first launch); `cold`, the 1 GiB "
-          "fill that evicts the L2s and the MALL; `in sequence`, a library GEMM or another "
-          "generated kernel, as inside a forward (the hipGraph replays, and the plan prefixes the "
-          "timing loop replays). Fractions are algorithmic bytes per launch over the mean "
-          "traced duration.", "", report(split, nbytes), "",
+          "loop: inputs cache-resident after the first launch); `in sequence`, a library GEMM or "
+          "another generated kernel, as inside a forward (the hipGraph replays, and the plan "
+          "prefixes the timing loop replays). Fractions are algorithmic bytes per launch over "
+          "the mean traced duration.", "", report(split, nbytes), "",
           "| symbol | launches per forward | kernel | algorithmic MB |", "|---|---:|---|---:|"]
     for sym, (k, alg, n) in sorted(info.items(), key=lambda kv: -kv[1][1] * kv[1][2]):
         L.append(f"| `{sym}` | {n} | {k.summary().split(': ', 1)[1][:60]} | {alg / 1e6:.2f} |")

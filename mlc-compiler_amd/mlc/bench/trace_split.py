@@ -1,19 +1,21 @@
-"""Split a ``rocprofv3 --kernel-trace`` of ``bench.py`` by what ran just before
-each generated-kernel dispatch:
+"""Split a ``rocprofv3 --kernel-trace`` by what ran just before each
+generated-kernel dispatch:
 
-* ``loop``: the same kernel (the back-to-back timing loop: inputs stay in the
-  256 MB MALL after the first launch);
-* ``cold``: a torch fill kernel (``bench.py``'s cache-evicting 1 GiB fill:
-  inputs come from HBM);
+* ``loop``: the same kernel (a back-to-back timing loop, such as
+  ``bench.py``'s per-kernel table: the inputs stay cache-resident after the
+  first launch);
+* ``after fill``: a torch fill kernel (a measurement that writes a large
+  buffer before a launch to evict the caches);
 * ``in sequence``: anything else -- a library GEMM or another generated
-  kernel, as inside a forward (the hipGraph replays, and the plan prefixes the
+  kernel, as inside a forward (the hipGraph replays, and the plan prefixes a
   timing loop replays before each kernel).
 
     python mlc-compiler_amd/mlc/bench/trace_split.py <kernel_trace.csv> [--bytes BYTES.json]
 
 Prints a markdown table: per generated function, the dispatch count and the
-mean duration of each class (and, with ``--bytes``, a JSON map from symbol to
-algorithmic bytes per launch, the bandwidth of each class).
+mean traced duration of each class that occurs (and, with ``--bytes``, a JSON
+map from symbol to algorithmic bytes per launch, each class's fraction of
+8 TB/s).
 """
 
 from __future__ import annotations
@@ -25,6 +27,7 @@ import statistics
 import sys
 
 HBM_PEAK_GBS = 8000.0
+KINDS = ("loop", "after fill", "in sequence")
 
 
 def classify(rows: list[dict]) -> dict[str, dict[str, list[float]]]:
@@ -38,7 +41,7 @@ def classify(rows: list[dict]) -> dict[str, dict[str, list[float]]]:
             if before == name:
                 kind = "loop"
             elif "FillFunctor" in before:
-                kind = "cold"
+                kind = "after fill"
             else:
                 kind = "in sequence"
             us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
@@ -48,10 +51,10 @@ def classify(rows: list[dict]) -> dict[str, dict[str, list[float]]]:
 
 
 def report(split, nbytes: dict | None = None) -> str:
-    kinds = ("loop", "cold", "in sequence")
+    kinds = [k for k in KINDS if any(k in d for d in split.values())]
     head = "| symbol | " + " | ".join(f"{k}: n, avg us" for k in kinds) + " |"
     if nbytes:
-        head += " " + " | ".join(f"{k} frac of 8 TB/s" for k in kinds) + " |"
+        head += " " + " | ".join(f"{k}: of 8 TB/s" for k in kinds) + " |"
     lines = [head, "|---" * (1 + len(kinds) * (2 if nbytes else 1)) + "|"]
     for sym in sorted(split, key=lambda s: -(nbytes or {}).get(s, 0)):
         cells, fracs = [], []

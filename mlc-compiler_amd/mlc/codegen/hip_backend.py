@@ -560,10 +560,10 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
         return lines, r
 
     # -- vector path: the pack's loads, then its arithmetic and stores --
-    def pack_loads(e0: str, sfx: str) -> list[str]:
+    def pack_loads(e0: str) -> list[str]:
         out = []
         for i, (a, acc) in enumerate(zip(k.inputs, accesses)):
-            ct, v = in_types[i], f"v{i}{sfx}"
+            ct, v = in_types[i], f"v{i}"
             if acc.mode == "uniform":
                 out.append(f"    const {ct} {v} = mlc::ld(in{i} + {offset(a, e0)});")
             elif acc.mode == "affine" and acc.aligned:
@@ -579,10 +579,10 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
                 out.append(f"    for (int j = 0; j < V; ++j) {v}[j] = mlc::ld(in{i} + {offset(a, '(' + e0 + ' + (' + it + ')j)')});")
         return out
 
-    def pack_compute_store(e0: str, sfx: str) -> list[str]:
+    def pack_compute_store(e0: str) -> list[str]:
         def ref_vec(slot):
             mode = accesses[slot].mode
-            return (f"v{slot}{sfx}" if mode == "uniform" else f"v{slot}{sfx}[j]"), in_types[slot]
+            return (f"v{slot}" if mode == "uniform" else f"v{slot}[j]"), in_types[slot]
 
         out = []
         for i, a in enumerate(k.outputs):
@@ -605,7 +605,7 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
 
     L.append(f"  const {it} e0 = base * V;")
     L.append("  if (e0 >= N) return;")
-    vec = pack_loads("e0", "") + pack_compute_store("e0", "")
+    vec = pack_loads("e0") + pack_compute_store("e0")
 
     if exact:
         L.append("  {")

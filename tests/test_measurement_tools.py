@@ -23,16 +23,18 @@ def test_dispatches_are_classified_by_their_predecessor():
         _row("mlc_a", 17_000, 20_000),        # after itself: loop, 3 us
         _row("mlc_a", 21_000, 24_000),        # loop, 3 us
         _row(fill, 25_000, 225_000),
-        _row("mlc_a", 226_000, 233_000),      # after the fill: cold, 7 us
+        _row("mlc_a", 226_000, 233_000),      # after the fill, 7 us
         _row("mlc_b", 234_000, 236_000),      # after another generated kernel: in sequence
     ]
     # out of order on input: classification follows start time
     split = classify(list(reversed(rows)))
-    assert split["mlc_a"] == {"in sequence": [5.0], "loop": [3.0, 3.0], "cold": [7.0]}
+    assert split["mlc_a"] == {"in sequence": [5.0], "loop": [3.0, 3.0], "after fill": [7.0]}
     assert split["mlc_b"] == {"in sequence": [2.0]}
     table = report(split, {"mlc_a": 24_000_000})
     # 24 MB in 3 us is 8 TB/s: the loop column reads 1.000 of peak
     assert "| `mlc_a` | 2, 3.00 | 1, 7.00 | 1, 5.00 | 1.000 | 0.429 | 0.600 |" in table
+    # classes that never occur are left out of the table
+    assert "after fill" not in report({"mlc_c": {"loop": [1.0]}})
 
 
 def test_loop_durations_take_only_back_to_back_dispatches():
