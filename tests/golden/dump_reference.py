@@ -21,6 +21,14 @@ built by ``ffn_block_config1``): ``reference_config1.json`` (schedule, arena
 plan, output shape) and ``reference_config1_out.npy`` (the reference's
 torch-backend output on the CPU, float32).
 
+    python tests/golden/dump_reference.py /root/reference tests/golden --outputs
+
+The third form writes ``reference_outputs_fp16.npz``: the reference's
+torch-backend outputs on the CPU for BASELINE configs 2-4 (BERT-base fp16 b1
+and b32 pooled outputs in full; GPT-2 small fp16 b1 logits as every 101st
+element of the flattened tensor, plus each of its 128 rows' sum and maximum
+in float64), from this repository's seeded workloads.
+
 The reference is imported from the path given; the script runs in its own
 process so the reference's ``mlc`` package never meets this repository's.
 """
@@ -180,8 +188,40 @@ def main_config1(ref_root: str, out_dir: str) -> None:
     print("config1", sched.counts(), sched.plan.arena_bytes, flush=True)
 
 
+def main_outputs(ref_root: str, out_dir: str) -> None:
+    sys.path.insert(0, ref_root)
+    import numpy as np
+    import torch
+
+    import mlc
+    from mlc.config import Config
+
+    build = _load(REPO / "mlc-compiler_amd" / "mlc" / "bench" / "models.py",
+                  "repo_bench_models").build
+    arrays = {"torch_version": np.array(torch.__version__)}
+    for key, name, batch in (("C2", "bert-base", 1), ("C4", "bert-base", 32),
+                             ("C3", "gpt2-small", 1)):
+        model, args = build(name, batch, 128, "cpu", torch.float16, init="normal")
+        compiled = mlc.compile(model, args, Config())
+        out = compiled(*args)
+        out = (out if isinstance(out, torch.Tensor) else out[0]).detach()
+        arrays[f"{key}_shape"] = np.array(list(out.shape))
+        if key == "C3":
+            flat = out.reshape(-1)
+            arrays[f"{key}_sample"] = flat[::101].numpy()
+            rows = out.double().reshape(-1, out.shape[-1])
+            arrays[f"{key}_row_sum"] = rows.sum(dim=1).numpy()
+            arrays[f"{key}_row_max"] = rows.max(dim=1).values.numpy()
+        else:
+            arrays[f"{key}_out"] = out.numpy()
+        print(key, compiled.backend, tuple(out.shape), out.dtype, flush=True)
+    np.savez_compressed(pathlib.Path(out_dir) / "reference_outputs_fp16.npz", **arrays)
+
+
 if __name__ == "__main__":
     if len(sys.argv) > 3 and sys.argv[3] == "--config1":
         main_config1(sys.argv[1], sys.argv[2])
+    elif len(sys.argv) > 3 and sys.argv[3] == "--outputs":
+        main_outputs(sys.argv[1], sys.argv[2])
     else:
         main(sys.argv[1], sys.argv[2])

@@ -104,6 +104,34 @@ def test_oracle_matches_reference_backend_on_config1():
     torch.testing.assert_close(got.reshape(-1), want, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("key", ["C2", "C3", "C4"])
+def test_oracle_matches_reference_backend_on_fp16_models(key):
+    """BASELINE configs 2-4 (BERT-base fp16 b1 and b32 pooled outputs, GPT-2
+    small fp16 b1 logits): the oracle against the reference torch backend's
+    own outputs, written by the reference compiler on this image's CPU
+    (``tests/golden/reference_outputs_fp16.npz``: BERT in full; GPT-2 as every
+    101st logit and each row's float64 sum and maximum). Bit for bit: both run
+    the same torch CPU ops (fp16 storage, fp32 arithmetic) in the same order."""
+    import numpy as np
+
+    from mlc.bench.workloads import make
+
+    ref = np.load(GOLDEN.parent / "reference_outputs_fp16.npz", allow_pickle=False)
+    if str(ref["torch_version"]) != torch.__version__:
+        pytest.skip(f"fixture was written with torch {ref['torch_version']}")
+    model, args = make(key, "cpu")
+    out = compile_reference(model, args)(*args)
+    out = out if isinstance(out, torch.Tensor) else out[0]
+    assert list(out.shape) == ref[f"{key}_shape"].tolist() and out.dtype == torch.float16
+    if key == "C3":
+        assert torch.equal(out.reshape(-1)[::101], torch.from_numpy(ref["C3_sample"]))
+        rows = out.double().reshape(-1, out.shape[-1])
+        assert np.array_equal(rows.sum(dim=1).numpy(), ref["C3_row_sum"])
+        assert np.array_equal(rows.max(dim=1).values.numpy(), ref["C3_row_max"])
+    else:
+        assert torch.equal(out, torch.from_numpy(ref[f"{key}_out"]))
+
+
 @pytest.mark.parametrize("name", [m[0] for m in all_models()])
 def test_exactness_classes_are_bit_identical(name):
     """Configs without reduction fusion evaluate the same ops in the same
