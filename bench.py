@@ -26,8 +26,9 @@ alone; ``mlc.bench.launch_floor``), and ``roofline.in_forward`` gives the
 dominant kernel's excess per launch the same way.
 ``schedule_variants`` times the opt-in schedule changes (never the headline
 value). The CPU baseline is the oracle (the kernel IR executed with torch on
-the host) on a bounded number of forwards of every config. Prints one JSON
-line.
+the host) on a bounded number of forwards of every config. ``parity`` holds the
+GPU outputs' distance from that oracle and from the reference compiler's own
+outputs (a committed fixture). Prints one JSON line.
 """
 
 from __future__ import annotations
@@ -309,6 +310,35 @@ def _cpu_baseline(hip_outputs: dict, budget_s: float, with_c5: bool = True):
     }, parity
 
 
+def _reference_fixture_errors(hip_outputs: dict) -> dict:
+    """The GPU outputs timed above against the reference compiler's own
+    outputs for configs 2-4 (``tests/golden/reference_outputs_fp16.npz``,
+    written by the reference's torch backend on a CPU): max error relative to
+    the reference's largest magnitude; GPT-2's logits on the fixture's sample
+    of every 101st value."""
+    import numpy as np
+    import torch
+
+    path = ROOT / "tests" / "golden" / "reference_outputs_fp16.npz"
+    if not path.exists():
+        return {}
+    ref = np.load(path, allow_pickle=False)
+    errs = {}
+    for key in ("C2", "C3", "C4"):
+        got = hip_outputs.get(key)
+        if got is None:
+            continue
+        if key == "C3":
+            got, want = got.reshape(-1)[::101], torch.from_numpy(ref["C3_sample"]).float()
+        else:
+            want = torch.from_numpy(ref[f"{key}_out"]).float()
+        got, want = got.double(), want.double()
+        errs[key] = round((got - want).abs().max().item() / want.abs().max().item(), 6)
+    errs["bar"] = {"C2": 3e-3, "C3": 2e-3, "C4": 3e-3}
+    errs["north_star_bar"] = 2e-3
+    return errs
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -345,7 +375,7 @@ def main() -> int:
         model, inputs = make(key, "cuda")
         compiled = mlc.compile(model, inputs, Config())
         results[key] = _time_replays(compiled, inputs, opts.steps, opts.warmup)
-        if key in ("C2", "C4"):
+        if key in ("C2", "C3", "C4"):
             out = compiled(*inputs)
             outputs[key] = (out if isinstance(out, torch.Tensor) else out[0]).float().cpu()
         results[key]["kernels"] = compiled.schedule.counts()
@@ -477,6 +507,8 @@ def main() -> int:
             "b1": checked.get("C2"), "b32": checked.get("C4"), "bar": 3e-3,
             "north_star_bar": 2e-3,
             "measure": "max|hip - oracle| / max|oracle|, oracle on the CPU (its own GEMMs)"}}
+    line["parity"] = line["parity"] or {}
+    line["parity"]["vs_reference_outputs"] = _reference_fixture_errors(outputs)
     print(json.dumps(line), flush=True)
     return 0
 
