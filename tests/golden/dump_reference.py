@@ -24,10 +24,11 @@ torch-backend output on the CPU, float32).
     python tests/golden/dump_reference.py /root/reference tests/golden --outputs
 
 The third form writes ``reference_outputs_fp16.npz``: the reference's
-torch-backend outputs on the CPU for BASELINE configs 2-4 (BERT-base fp16 b1
+torch-backend outputs on the CPU for BASELINE configs 2-5 (BERT-base fp16 b1
 and b32 pooled outputs in full; GPT-2 small fp16 b1 logits as every 101st
 element of the flattened tensor, plus each of its 128 rows' sum and maximum
-in float64), from this repository's seeded workloads.
+in float64; GPT-2 b32 s512 logits as every 10007th element plus each of its
+16,384 rows' maximum), from this repository's seeded workloads.
 
 The reference is imported from the path given; the script runs in its own
 process so the reference's ``mlc`` package never meets this repository's.
@@ -199,9 +200,9 @@ def main_outputs(ref_root: str, out_dir: str) -> None:
     build = _load(REPO / "mlc-compiler_amd" / "mlc" / "bench" / "models.py",
                   "repo_bench_models").build
     arrays = {"torch_version": np.array(torch.__version__)}
-    for key, name, batch in (("C2", "bert-base", 1), ("C4", "bert-base", 32),
-                             ("C3", "gpt2-small", 1)):
-        model, args = build(name, batch, 128, "cpu", torch.float16, init="normal")
+    for key, name, batch, seq in (("C2", "bert-base", 1, 128), ("C4", "bert-base", 32, 128),
+                                  ("C3", "gpt2-small", 1, 128), ("C5", "gpt2-small", 32, 512)):
+        model, args = build(name, batch, seq, "cpu", torch.float16, init="normal")
         compiled = mlc.compile(model, args, Config())
         out = compiled(*args)
         out = (out if isinstance(out, torch.Tensor) else out[0]).detach()
@@ -212,6 +213,9 @@ def main_outputs(ref_root: str, out_dir: str) -> None:
             rows = out.double().reshape(-1, out.shape[-1])
             arrays[f"{key}_row_sum"] = rows.sum(dim=1).numpy()
             arrays[f"{key}_row_max"] = rows.max(dim=1).values.numpy()
+        elif key == "C5":
+            arrays[f"{key}_sample"] = out.reshape(-1)[::10007].numpy()
+            arrays[f"{key}_row_max"] = out.reshape(-1, out.shape[-1]).max(dim=1).values.numpy()
         else:
             arrays[f"{key}_out"] = out.numpy()
         print(key, compiled.backend, tuple(out.shape), out.dtype, flush=True)
