@@ -22,7 +22,9 @@ Pinning (what fixes this oracle independently of itself):
 * end-to-end equality with eager PyTorch on every toy model under every pass
   configuration at the reference's tolerances (rtol 1e-5 / atol 1e-6 fp32),
   and the reference's own torch-backend outputs for the same inputs
-  (fixtures it wrote), ``tests/test_oracle.py``;
+  (fixtures it wrote), ``tests/test_oracle.py``; for BASELINE configs 1-4
+  (the fp32 FFN block, BERT-base fp16 b1 and b32, GPT-2 small fp16 b1) those
+  outputs are reproduced bit for bit;
 * seeded random programs (pointwise chains, views, casts, reductions, extern
   GEMMs, transformer stacks) against eager PyTorch, ``tests/test_fuzz.py``;
 * the reference's index-rendering known answers (``tests/test_codegen.py``);
