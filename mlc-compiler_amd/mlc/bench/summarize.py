@@ -4,6 +4,8 @@
         --fetch DIR --write DIR --trace DIR [--config every] --title TEXT -o profiles/X.md
     python mlc-compiler_amd/mlc/bench/summarize.py stats --trace DIR --command TEXT \\
         --title TEXT -o profiles/X.md
+    python mlc-compiler_amd/mlc/bench/summarize.py counters --kind valu|stalls \\
+        --workload C4 --pmc DIR [--pmc DIR] --trace DIR --title TEXT -o profiles/X.md
 
 ``traffic``: the ``FETCH_SIZE`` and ``WRITE_SIZE`` runs of ``traffic.py --kernel
 all`` (one counter per run) and a kernel trace of the same tool. Each counter
@@ -19,6 +21,11 @@ reads for its ``traffic`` field.
 of rocprofv3's own per-kernel table, then every generated function of BERT
 b32 with its dispatches split by what ran just before (``trace_split``: the
 timing loop, or in sequence as in a forward).
+
+``counters``: per generated function, the means of a ``--pmc`` run's counters
+over its launches inside the forward: VALU issue against traced time
+(``--kind valu``), or the shares of its waves' lifetime spent waiting and the
+texture-path stall cycles (``--kind stalls``).
 
 Symbols are matched to kernels by compiling the workload's schedule on the CPU
 (the symbol is a hash of the generated function's body).
@@ -197,6 +204,118 @@ def stats(opts) -> str:
     return "\n".join(L) + "\n"
 
 
+def _counters(directories: list[str]) -> dict:
+    """symbol -> counter name -> [(dispatch id, value)] over several PMC runs."""
+    by: dict = collections.defaultdict(lambda: collections.defaultdict(list))
+    for d in directories:
+        for r in _csv(d, "counter_collection.csv"):
+            by[r["Kernel_Name"].split("(")[0].strip()][r["Counter_Name"]].append(
+                (int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+    return by
+
+
+#: cycles per wave64 fp32 VALU instruction on a 16-lane SIMD (packed fp32 off),
+#: SIMDs on the chip, and the shader clock used to turn issue counts into time
+VALU_CYCLES, SIMDS, CLOCK_HZ = 4, 1024, 2.4e9
+
+VALU_COUNTERS = ("SQ_WAVES SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_VMEM_RD SQ_INSTS_VMEM_WR "
+                 "SQ_INSTS_LDS SQ_BUSY_CYCLES SQ_WAVE_CYCLES",
+                 "SQ_INSTS_VALU_ADD_F32 SQ_INSTS_VALU_CVT SQ_INSTS_VALU_FMA_F32 "
+                 "SQ_INSTS_VALU_MFMA_F32 SQ_INSTS_VALU_MUL_F32 SQ_INSTS_VALU_TRANS_F16 "
+                 "SQ_INSTS_VALU_TRANS_F32")
+STALL_COUNTERS = ("SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY "
+                  "SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_ANY SQ_INSTS_VALU",
+                  "TA_BUSY_avr TA_DATA_STALLED_BY_TC_CYCLES_sum TCP_PENDING_STALL_CYCLES_sum "
+                  "TCP_TCR_TCP_STALL_CYCLES_sum TCP_READ_TAGCONFLICT_STALL_CYCLES_sum "
+                  "TCP_TCP_TA_DATA_STALL_CYCLES_sum GRBM_GUI_ACTIVE")
+
+
+def counters(opts) -> str:
+    """``valu``: VALU issue against traced time per generated function;
+    ``stalls``: where its waves wait. Each counter is the mean over the
+    function's first ``n`` dispatches (``n`` = its launches per forward:
+    ``traffic.py`` runs one whole forward before its timing loops, so those
+    are the launches inside the forward, on their real inputs)."""
+    info = schedule_symbols(opts.workload, opts.config == "every")
+    by = _counters(opts.pmc)
+    loop = _loop_us(_csv(opts.trace, "kernel_trace.csv"))
+    sets = VALU_COUNTERS if opts.kind == "valu" else STALL_COUNTERS
+    tool = ("python3 -u $R/mlc-compiler_amd/mlc/bench/traffic.py --kernel all"
+            + (" --config every" if opts.config == "every" else "")
+            + f" --workload {opts.workload}")
+    L = [f"# {opts.title}", "", "Commands (run from `/tmp` on the MI355X box, repository at "
+         "`$R`; one counter set per run):", "", "```"]
+    for d, names in zip(opts.pmc, sets):
+        L += [f"rocprofv3 --pmc {names} --output-format csv -d {_show(d)} -o v -- \\",
+              f"    {tool} --iters 3 --copy-mib 64"]
+    L += [f"rocprofv3 --kernel-trace --stats --output-format csv -d {_show(opts.trace)} -o t -- "
+          "\\", f"    {tool} --iters 20 --copy-mib 64",
+          f"python3 $R/mlc-compiler_amd/mlc/bench/summarize.py counters --kind {opts.kind} "
+          f"--workload {opts.workload} --config {opts.config} "
+          + " ".join(f"--pmc {_show(d)}" for d in opts.pmc)
+          + f" --trace {_show(opts.trace)} --title '<title>' -o <summary.md>", "```", ""]
+    rows = []
+    for sym, (k, nbytes, n) in info.items():
+        c = by.get(sym)
+        if not c:
+            continue
+        def f(name, c=c, n=n):
+            return statistics.mean(v for _, v in sorted(c[name])[:n])
+
+        t = statistics.mean(loop[sym]) if loop.get(sym) else float("nan")
+        rows.append((n, sym, k.summary().split(": ", 1)[1], nbytes, f, t))
+    rows.sort(key=lambda r: -r[0] * (r[5] if r[5] == r[5] else 0))
+    if opts.kind == "valu":
+        L += ["Counters are each function's launches inside the forward (real inputs); the time "
+              "is the traced average of its back-to-back launches (tracing adds about 0.8 us). "
+              "VALU issue time = `SQ_INSTS_VALU` x 4 cycles (a wave64 fp32 VALU instruction on a "
+              "16-lane SIMD; packed fp32 is off) / 1024 SIMDs / 2.4 GHz: the time the kernel "
+              "would take if it did nothing but issue its vector ALU instructions on every SIMD "
+              "of the chip. The `SQ_INSTS_VALU_*` classes are per wave; `v_fma_mix_f32` counts "
+              "as FMA_F32.", "",
+              "| n | symbol | kernel | MB / launch | waves | VALU / wave | TRANS | FMA | ADD | MUL "
+              "| CVT | VMEM / wave | VALU issue us | traced us |",
+              "|---:|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+        for n, sym, summ, nbytes, f, t in rows:
+            waves = f("SQ_WAVES")
+            valu = f("SQ_INSTS_VALU")
+            def per(name, f=f, waves=waves):
+                return f(name) / waves
+
+            issue = valu * VALU_CYCLES / SIMDS / CLOCK_HZ * 1e6
+            vmem = (f("SQ_INSTS_VMEM_RD") + f("SQ_INSTS_VMEM_WR")) / waves
+            L.append(f"| {n} | `{sym}` | {summ[:50]} | {nbytes / 1e6:.2f} | {waves:.0f} | "
+                     f"{valu / waves:.1f} | {per('SQ_INSTS_VALU_TRANS_F32'):.1f} | "
+                     f"{per('SQ_INSTS_VALU_FMA_F32'):.1f} | {per('SQ_INSTS_VALU_ADD_F32'):.1f} | "
+                     f"{per('SQ_INSTS_VALU_MUL_F32'):.1f} | {per('SQ_INSTS_VALU_CVT'):.1f} | "
+                     f"{vmem:.1f} | {issue:.2f} | {t:.2f} |")
+    else:
+        L += ["Each function's launches inside the forward (real inputs). The SQ columns are "
+              "shares of the waves' lifetime (`SQ_WAVE_CYCLES`): waiting on anything "
+              "(`SQ_WAIT_ANY`), waiting for an instruction's dependency (`SQ_WAIT_INST_ANY`), "
+              "issuing VALU work, issuing anything. The TA/TCP columns are cycles per GPU-active "
+              "cycle (`GRBM_GUI_ACTIVE`), summed over the chip's instances (`TA_BUSY_avr` "
+              "averaged): texture-address busy, texture-address data stalled by the L2 "
+              "(`TA_DATA_STALLED_BY_TC`), vector L1 stalled on pending misses "
+              "(`TCP_PENDING_STALL`), on the L2 return path (`TCP_TCR_TCP_STALL`), on tag "
+              "conflicts, and on the TA data path.", "",
+              "| n | symbol | kernel | waves | wait any | wait inst | VALU | issue any | TA busy "
+              "| TA data stalled by L2 | TCP pending stall | TCP L2-return stall | TCP tag conflict "
+              "| TCP TA-data stall |",
+              "|---:|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+        for n, sym, summ, nbytes, f, t in rows:
+            wc, g = f("SQ_WAVE_CYCLES"), f("GRBM_GUI_ACTIVE")
+            L.append(f"| {n} | `{sym}` | {summ[:44]} | {f('SQ_WAVES'):.0f} | "
+                     f"{f('SQ_WAIT_ANY') / wc:.0%} | {f('SQ_WAIT_INST_ANY') / wc:.0%} | "
+                     f"{f('SQ_ACTIVE_INST_VALU') / wc:.0%} | {f('SQ_ACTIVE_INST_ANY') / wc:.0%} | "
+                     f"{f('TA_BUSY_avr') / g:.2f} | {f('TA_DATA_STALLED_BY_TC_CYCLES_sum') / g:.2f} | "
+                     f"{f('TCP_PENDING_STALL_CYCLES_sum') / g:.2f} | "
+                     f"{f('TCP_TCR_TCP_STALL_CYCLES_sum') / g:.2f} | "
+                     f"{f('TCP_READ_TAGCONFLICT_STALL_CYCLES_sum') / g:.2f} | "
+                     f"{f('TCP_TCP_TA_DATA_STALL_CYCLES_sum') / g:.2f} |")
+    return "\n".join(L) + "\n"
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="what", required=True)
@@ -214,8 +333,17 @@ def main() -> int:
     s.add_argument("--title", required=True)
     s.add_argument("--top", type=int, default=30)
     s.add_argument("-o", "--out", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("--kind", choices=("valu", "stalls"), required=True)
+    c.add_argument("--workload", required=True)
+    c.add_argument("--config", choices=("reference", "every"), default="reference")
+    c.add_argument("--pmc", action="append", required=True,
+                   help="a PMC run's output directory (the counter sets of --kind, in order)")
+    c.add_argument("--trace", required=True)
+    c.add_argument("--title", required=True)
+    c.add_argument("-o", "--out", required=True)
     opts = ap.parse_args()
-    text = traffic(opts) if opts.what == "traffic" else stats(opts)
+    text = {"traffic": traffic, "stats": stats, "counters": counters}[opts.what](opts)
     pathlib.Path(opts.out).write_text(text)
     print(text[-1500:])
     return 0
