@@ -90,7 +90,7 @@ class _FastExpRenderer(Renderer):
     rounding of ``b log2 e`` is the same factor on every exp of the row and
     cancels in the normalisation)."""
 
-    def call(self, e):
+    def _call(self, e):
         if e.fn == "exp":
             x = e.args[0]
             if isinstance(x, Ref) and isinstance(self.defs.get(x.name), Call):
@@ -102,7 +102,7 @@ class _FastExpRenderer(Renderer):
             code, t = self(x)
             if t == "float":
                 return f"mlc::exp_fast({code})", "float"
-        return super().call(e)
+        return super()._call(e)
 
 
 #: 16-bit element, 8- and 4-element vector types of the operands, per dtype

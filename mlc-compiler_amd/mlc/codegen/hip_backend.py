@@ -6,9 +6,11 @@ This replaces the reference's Triton emitters
 (``mlc/codegen/triton_backend.py:206-287``, ``triton_reduction.py:73-274``)
 behind the same seam: it consumes the kernel IR (``PointwiseKernel`` /
 ``ReductionKernel``) and returns source plus a launch table. Semantics kept
-from the reference: narrow floats load into fp32 registers, all arithmetic is
-fp32, stores round back to the buffer dtype (round-to-nearest-even); reduce
-identities neutralise masked lanes; row-constant operands are scalar loads.
+from the reference: narrow floats load into fp32 registers, arithmetic is
+fp32, stores round back to the buffer dtype (round-to-nearest-even); after an
+explicit cast to fp16 or bf16 each result is rounded to that type, as the
+reference's torch evaluation rounds it (``value_types``); reduce identities
+neutralise masked lanes; row-constant operands are scalar loads.
 
 The MI355X design:
 
@@ -46,6 +48,7 @@ from ..kernels import AttentionKernel, Bind, ExternKernel, PointwiseKernel, Redu
 from ..ir.graph import Value
 from .index import IndexMap, build_index
 from .reduction_schedule import plan_passes, scalar_binds, varies_by_column
+from .value_types import ROUND, VType, expr_type, kernel_types, load_type
 
 WAVE = 64
 
@@ -118,7 +121,8 @@ class Renderer:
     operations would round once too).
     """
 
-    def __init__(self, operand, temp, half_slots=frozenset(), defs=None, to_fp16=frozenset()) -> None:
+    def __init__(self, operand, temp, half_slots=frozenset(), defs=None, to_fp16=frozenset(),
+                 vtypes=None) -> None:
         self.operand = operand
         self.temp = temp
         self.half_slots = frozenset(half_slots)
@@ -126,6 +130,11 @@ class Renderer:
         #: temporaries whose every use rounds them to fp16
         self.to_fp16 = frozenset(to_fp16)
         self._plain = False
+        #: (input types by slot, temporary types by name) as the reference's
+        #: torch evaluation holds them (``value_types``): a call whose result
+        #: is typed fp16 or bf16 is rounded to that type
+        self.vtypes = vtypes
+        self._vmemo: dict[int, VType] = {}
 
     def bind(self, name: str, e: Expr) -> tuple[str, str]:
         """Render the defining expression of temporary ``name``. An add, sub
@@ -228,7 +237,22 @@ class Renderer:
             return f"((int64_t){v}LL)", "int64_t"
         return float_literal(float(v)), "float"
 
+    def value_type(self, e: Expr) -> VType | None:
+        if self.vtypes is None:
+            return None
+        ins, temps = self.vtypes
+        return expr_type(e, ins.__getitem__, lambda n: temps.get(n, (torch.float32, True)),
+                         self._vmemo)
+
     def call(self, e: Call) -> tuple[str, str]:
+        code, t = self._call(e)
+        if t == "float":
+            nt = self.value_type(e)
+            if nt is not None and nt[0] in ROUND:
+                code = f"{ROUND[nt[0]]}({code})"
+        return code, t
+
+    def _call(self, e: Call) -> tuple[str, str]:
         plain, self._plain = self._plain, False
         args = [self(a) for a in e.args]
         codes = [c for c, _ in args]
@@ -276,6 +300,8 @@ class Renderer:
             t = "double" if top == "double" else "float"
             return f"mlc::pow_(({t})({a}), ({t})({codes[1]}))", t
         if fn == "neg":
+            if types[0] == "float":
+                return f"mlc::neg_({a})", "float"
             return f"(-({a}))", "int64_t" if types[0] == "bool" else types[0]
         if fn == "abs":
             return f"mlc::abs_({a})", types[0]
@@ -295,6 +321,23 @@ class Renderer:
 def half_inputs(k) -> frozenset[int]:
     """Input slots stored as fp16 (read into fp32 registers by conversion)."""
     return frozenset(i for i, a in enumerate(k.inputs) if a.dtype == torch.float16)
+
+
+def value_types_of(k, online: frozenset[str] = frozenset()):
+    """(input types, temporary types) of ``k`` for ``Renderer``."""
+    return [load_type(a.dtype) for a in k.inputs], kernel_types(k, online)
+
+
+def narrow_values(vt) -> frozenset[str]:
+    """Temporaries typed fp16 or bf16: no fp32 shortcut may skip their rounding."""
+    return frozenset(n for n, t in vt[1].items() if t[0] in ROUND)
+
+
+def _reduced(step: Reduce, vt, code: str) -> str:
+    """A row reduction's result, rounded to its type when that is fp16 or
+    bf16 (torch reduces a narrow tensor in fp32 and rounds once)."""
+    t = vt[1][step.name][0]
+    return f"{ROUND[t]}({code})" if t in ROUND else code
 
 
 def bind_defs(k: ReductionKernel) -> dict[str, Expr]:
@@ -549,10 +592,11 @@ def emit_pointwise(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
     half_slots = half_inputs(k)
     defs = dict(k.body)
     to_fp16 = fp16_rounded(k)
+    vt = value_types_of(k)
 
     def body_lines(ref_in, indent: str) -> list[str]:
         lines = []
-        r = Renderer(ref_in, lambda n: (n, temp_types[n]), half_slots, defs, to_fp16)
+        r = Renderer(ref_in, lambda n: (n, temp_types[n]), half_slots, defs, to_fp16, vt)
         for name, expr in k.body:
             code, t = r.bind(name, expr)
             temp_types[name] = t
@@ -718,7 +762,7 @@ def emit_transpose(k: PointwiseKernel, cfg: Config | None = None) -> tuple[str, 
     def operand(s_: int):
         return ("x0" if s_ == slot else f"xr{s_}"), in_types[s_]
 
-    r = Renderer(operand, lambda n: (n, temp_types[n]))
+    r = Renderer(operand, lambda n: (n, temp_types[n]), vtypes=value_types_of(k))
     body = []
     for name, expr in k.body:
         code, t = r(expr)
@@ -992,9 +1036,11 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
 
     nonpos = nonpositive_args(k)
     half_slots, defs, to_fp16 = half_inputs(k), bind_defs(k), fp16_rounded(k)
+    vt = value_types_of(k)
+    narrow = narrow_values(vt)
     elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos, half_slots, defs, to_fp16,
-                                fast_softmax_exps(k, nonpos))
-    scal_r = Renderer(ref_scalar, temp_scalar, half_slots, defs, to_fp16)
+                                fast_softmax_exps(k, nonpos) - narrow, vt)
+    scal_r = Renderer(ref_scalar, temp_scalar, half_slots, defs, to_fp16, vt)
     rcp_for = _reciprocal_divisors(k, vector)
 
     def elem_loop(target: str, code: str) -> list[str]:
@@ -1007,7 +1053,7 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
                 code, t = elem_r.bind(s.name, s.expr)
                 temp_types[s.name] = t
                 L.append(f"  {t} {s.name}[K][V];")
-                sd = _scalar_division(s.expr, rcp_for)
+                sd = _scalar_division(s.expr, rcp_for) if s.name not in narrow else None
                 if sd is not None and t == "float" and softmax_sum(k, sd[1], nonpos):
                     num, d = elem_r(sd[0])[0], sd[1]
                     L += elem_loop(s.name, _row_division(k, s.name, sd[0], num, d, nonpos))
@@ -1057,7 +1103,7 @@ def emit_persistent(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             L.append(f"      for (int j = 0; j < V; ++j) acc = {op}::f(acc, x);")
             L.append("    }")
         slot = f"lds_{s.name}" if G > WAVE else "nullptr"
-        L.append(f"    {s.name} = mlc::row_reduce<G, {op}>(acc, ({t}*){slot});")
+        L.append(f"    {s.name} = {_reduced(s, vt, f'mlc::row_reduce<G, {op}>(acc, ({t}*){slot})')};")
         L.append("  }")
         L += _reciprocal_lines(s.name, rcp_for)
 
@@ -1230,8 +1276,8 @@ class _NonPosExpRenderer(Renderer):
     ``mlc::exp_fast_shift(x, rowmax)``."""
 
     def __init__(self, operand, temp, nonpos: set, half_slots=frozenset(), defs=None,
-                 to_fp16=frozenset(), fast=frozenset()) -> None:
-        super().__init__(operand, temp, half_slots, defs, to_fp16)
+                 to_fp16=frozenset(), fast=frozenset(), vtypes=None) -> None:
+        super().__init__(operand, temp, half_slots, defs, to_fp16, vtypes)
         self.nonpos = nonpos
         self.fast = frozenset(fast)
 
@@ -1245,12 +1291,12 @@ class _NonPosExpRenderer(Renderer):
                 return f"mlc::exp_fast_shift({x}, {m})", "float"
         return super().bind(name, e)
 
-    def call(self, e: Call) -> tuple[str, str]:
+    def _call(self, e: Call) -> tuple[str, str]:
         if e.fn == "exp" and e.args[0] in self.nonpos:
             code, t = self(e.args[0])
             if t == "float":
                 return f"mlc::exp_nonpos({code})", "float"
-        return super().call(e)
+        return super()._call(e)
 
 
 def _reciprocal_divisors(k: ReductionKernel, vector: set[str]) -> set[str]:
@@ -1349,8 +1395,13 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
 
     nonpos = nonpositive_args(k)
     half_slots, defs, to_fp16 = half_inputs(k), bind_defs(k), fp16_rounded(k)
-    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos, half_slots, defs, to_fp16)
-    scal_r = Renderer(lambda s: (f"v{s}", in_types[s]), temp_scalar, half_slots, defs, to_fp16)
+    online_names = frozenset(n for p in passes if p.online_softmax is not None
+                             for n in (p.online_softmax.max_step.name,
+                                       p.online_softmax.sum_step.name))
+    vt = value_types_of(k, online_names)
+    narrow = narrow_values(vt)
+    elem_r = _NonPosExpRenderer(ref_elem, temp_elem, nonpos, half_slots, defs, to_fp16, vtypes=vt)
+    scal_r = Renderer(lambda s: (f"v{s}", in_types[s]), temp_scalar, half_slots, defs, to_fp16, vt)
     rcp_for = _reciprocal_divisors(k, vector)
 
     def slots_for(p) -> list[int]:
@@ -1390,7 +1441,7 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
         for b in p.binds:
             code, t = elem_r.bind(b.name, b.expr)
             out.append(f"    {t} {b.name}[V];")
-            sd = _scalar_division(b.expr, rcp_for)
+            sd = _scalar_division(b.expr, rcp_for) if b.name not in narrow else None
             if sd is not None and t == "float" and softmax_sum(k, sd[1], nonpos):
                 num, d = elem_r(sd[0])[0], sd[1]
                 out.append("#pragma unroll")
@@ -1456,7 +1507,8 @@ def emit_streamed(k: ReductionKernel, cfg: Config) -> tuple[str, LaunchSpec]:
             for r in p.reduces:
                 t = temp_types[r.name]
                 slot = f"lds_{r.name}" if need_lds else "nullptr"
-                out.append(f"  const {t} {r.name} = mlc::row_reduce<G, {_OP[r.kind]}>(acc_{r.name}, ({t}*){slot});")
+                out.append(f"  const {t} {r.name} = "
+                           f"{_reduced(r, vt, f'mlc::row_reduce<G, {_OP[r.kind]}>(acc_{r.name}, ({t}*){slot})')};")
                 out += _reciprocal_lines(r.name, rcp_for)
         return out
 

@@ -249,6 +249,16 @@ __device__ __forceinline__ int64_t floor_(int64_t x) { return x; }
 __device__ __forceinline__ float abs_(float x) { return fabsf(x); }
 __device__ __forceinline__ double abs_(double x) { return fabs(x); }
 __device__ __forceinline__ int64_t abs_(int64_t x) { return x < 0 ? -x : x; }
+// fp32 negation: the sign bit flipped by one v_xor_b32. Written as an
+// instruction the compiler cannot see through because, with packed fp32 off,
+// ROCm 7.2's instruction selector fails on the negation of a value read from
+// bf16 storage when it pairs two such negations into a v2f32 operation
+// ("Cannot select: v2f32 = bitcast"). NaN's sign flips too, as in torch.
+__device__ __forceinline__ float neg_(float x) {
+  float r;
+  asm("v_xor_b32 %0, 0x80000000, %1" : "=v"(r) : "v"(x));
+  return r;
+}
 __device__ __forceinline__ float pow_(float a, float b) { return powf(a, b); }
 __device__ __forceinline__ double pow_(double a, double b) { return pow(a, b); }
 

@@ -179,11 +179,13 @@ def test_no_packed_fp32_by_hand_and_no_scalar_stores():
     text = src + native.TEMPLATES.joinpath("mlc_cdna4.h").read_text()
     assert not re.search(r"v_pk_(add|mul|fma)_f32", text)
     assert "-packed-fp32-ops" in native.HIP_FLAGS
-    # the one inline asm is an empty template that only hides a constant in
-    # an SGPR from the optimiser: it emits no instruction
+    # two inline asm statements: an empty template that only hides a constant
+    # in an SGPR from the optimiser (it emits no instruction), and fp32
+    # negation as one vector-register xor
     opaque = 'asm("" : "+s"(v));'
-    assert text.count(opaque) == 1
-    assert "asm" not in text.replace(opaque, "")
+    neg = 'asm("v_xor_b32 %0, 0x80000000, %1" : "=v"(r) : "v"(x));'
+    assert text.count(opaque) == 1 and text.count(neg) == 1
+    assert "asm" not in text.replace(opaque, "").replace(neg, "")
 
 
 @pytest.mark.parametrize("name,cfg", [("pre_norm_block", FULL), ("masked_softmax", STREAMED),
@@ -196,6 +198,26 @@ def test_module_cross_compiles_for_gfx950(name, cfg, tmp_path, monkeypatch):
     # cached: a second request does not recompile
     mtime = obj.stat().st_mtime_ns
     assert native.compile_code_object(mod.source)[1].stat().st_mtime_ns == mtime
+
+
+class _NegOfBf16(torch.nn.Module):
+    def forward(self, a, b):
+        return (-(a - b)).half(), -a
+
+
+def test_negation_of_bf16_values_cross_compiles(tmp_path, monkeypatch):
+    """Negating a value read from bf16 storage, with packed fp32 off, made
+    ROCm 7.2's instruction selector abort ("Cannot select: v2f32 = bitcast")
+    when the negation was written as a C++ minus: fp32 negation is emitted
+    as the header's sign-bit flip instead."""
+    monkeypatch.setenv("MLC_CACHE_DIR", str(tmp_path))
+    args = (torch.randn(4, 64).bfloat16(), torch.randn(4, 64).bfloat16())
+    sched = build_pipeline(capture(_NegOfBf16(), args), FULL)
+    mod = build_module(sched, FULL)
+    body = "".join(mod.functions.values())
+    assert "mlc::neg_(" in body and "(-(" not in body
+    _, obj = native.compile_code_object(mod.source)
+    assert obj.stat().st_size > 0
 
 
 def test_copy_ceiling_kernel_cross_compiles(tmp_path, monkeypatch):

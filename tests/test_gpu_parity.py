@@ -202,6 +202,36 @@ def test_mixed_precision_forms_are_bit_exact():
         assert torch.equal(g[ok].view(torch.int32), w[ok].view(torch.int32)), f"output {i}: bits"
 
 
+class _NegOfBf16(torch.nn.Module):
+    def forward(self, a, b):
+        return (-(a - b)).half(), -a
+
+
+def test_negation_of_bf16_values_is_exact():
+    """Negation of values read from bf16 storage (emitted as a sign-bit flip):
+    with bf16 specials (+-0, +-inf, NaN, a subnormal, values past the fp16
+    range) and random values, each output bit for bit equal to fp32
+    arithmetic on the CPU rounded once to the stored type, and the same NaN
+    positions."""
+    torch.manual_seed(0)
+    special = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), float("nan"), 1e-40,
+                            3e38, -3e38, 1.0, 70000.0, 1e-8])
+    vals = torch.cat([special, torch.randn(53) * 8]).bfloat16()
+    a = vals.repeat_interleave(64).view(64, 64)
+    b = vals.repeat(64).view(64, 64)
+    want = ((-(a.float() - b.float())).half(), -a)
+    compiled = mlc.compile(_NegOfBf16(), (a.cuda(), b.cuda()), Config(cuda_graphs=False))
+    assert "mlc::neg_(" in compiled._module.source
+    got = compiled(a.cuda(), b.cuda())
+    torch.cuda.synchronize()
+    for i, (g, w) in enumerate(zip(got, want)):
+        g = g.cpu()
+        assert g.dtype == w.dtype
+        assert torch.equal(torch.isnan(g), torch.isnan(w)), f"output {i}: NaN positions"
+        ok = ~torch.isnan(w)
+        assert torch.equal(g[ok].view(torch.int16), w[ok].view(torch.int16)), f"output {i}: bits"
+
+
 class _ShiftedExp(torch.nn.Module):
     def forward(self, x):
         return torch.exp(x - x.amax(dim=-1, keepdim=True))
