@@ -49,7 +49,8 @@ from ..kernels import AttentionKernel, Bind
 from .hip_backend import (_IDENTITY, _OP, STORAGE, WAVE, LaunchSpec, Renderer, _RowOffsets,
                           _expr_varies, _params, _reciprocal_divisors, _reciprocal_lines,
                           _row_col_access, _scalar_division, axis_terms, bind_defs, cast_code,
-                          compute_type, half_inputs, index_type, join_offset, render_terms)
+                          compute_type, half_inputs, index_type, join_offset, nonpositive_args,
+                          render_terms)
 from .reduction_schedule import varies_by_column
 
 #: the softmax's exp and its division by the row sum in fast forms
@@ -85,17 +86,24 @@ def attention_waves(heads: int, queries: int) -> int:
 
 
 class _FastExpRenderer(Renderer):
-    """``exp`` as ``mlc::exp_fast``; ``exp(a - b)`` as ``mlc::exp_fast_shift``
-    (one fma forms ``a log2 e - RN(b log2 e)``: with ``b`` a row's maximum the
-    rounding of ``b log2 e`` is the same factor on every exp of the row and
-    cancels in the normalisation)."""
+    """``exp`` as ``mlc::exp_fast``; ``exp(x - rowmax(x))`` as
+    ``mlc::exp_fast_shift`` (one fma forms ``x log2 e - RN(m log2 e)``: the
+    rounding of ``m log2 e`` for the row's maximum ``m`` is the same factor on
+    every exp of the row and cancels in the normalisation). ``nonpos`` holds
+    the ``x - rowmax(x)`` expressions (``nonpositive_args``); the exp of any
+    other difference keeps its own rounding and is ``exp_fast`` of it."""
+
+    def __init__(self, operand, temp, half_slots=frozenset(), defs=None, nonpos=frozenset()):
+        super().__init__(operand, temp, half_slots, defs)
+        self.nonpos = nonpos
 
     def _call(self, e):
         if e.fn == "exp":
             x = e.args[0]
+            shift = x in self.nonpos
             if isinstance(x, Ref) and isinstance(self.defs.get(x.name), Call):
                 x = self.defs[x.name]  # a bind holding the difference
-            if isinstance(x, Call) and x.fn == "sub":
+            if shift and isinstance(x, Call) and x.fn == "sub":
                 (a, ta), (b, tb) = self(x.args[0]), self(x.args[1])
                 if ta == "float" and tb == "float":
                     return f"mlc::exp_fast_shift({a}, {b})", "float"
@@ -391,10 +399,13 @@ def emit_attention(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpec]:
             raise AssertionError("vector temp read in a row-scalar expression")
         return name, temp_types[name]
 
-    R_ = _FastExpRenderer if FAST_SOFTMAX_MATH else Renderer
     half, defs = half_inputs(sm), bind_defs(sm)
-    elem_r = R_(ref_elem, temp_elem, half, defs)
-    scal_r = R_(ref_scalar, temp_scalar, half, defs)
+    if FAST_SOFTMAX_MATH:
+        nonpos = frozenset(nonpositive_args(sm))
+        elem_r = _FastExpRenderer(ref_elem, temp_elem, half, defs, nonpos)
+        scal_r = _FastExpRenderer(ref_scalar, temp_scalar, half, defs, nonpos)
+    else:
+        elem_r, scal_r = Renderer(ref_elem, temp_elem, half, defs), Renderer(ref_scalar, temp_scalar, half, defs)
     rcp_for = _reciprocal_divisors(sm, vector)
     score_cols = set(col_slots) | {k.score_slot}
 
@@ -659,9 +670,13 @@ def emit_attention_blocked(k: AttentionKernel, cfg=None) -> tuple[str, LaunchSpe
             raise AssertionError("vector temp read in a row-scalar expression")
         return name, temp_types[name]
 
-    R_ = _FastExpRenderer if FAST_SOFTMAX_MATH else Renderer
     half, defs = half_inputs(sm), bind_defs(sm)
-    elem_r, scal_r = R_(ref_elem, temp_elem, half, defs), R_(ref_scalar, temp_scalar, half, defs)
+    if FAST_SOFTMAX_MATH:
+        nonpos = frozenset(nonpositive_args(sm))
+        elem_r = _FastExpRenderer(ref_elem, temp_elem, half, defs, nonpos)
+        scal_r = _FastExpRenderer(ref_scalar, temp_scalar, half, defs, nonpos)
+    else:
+        elem_r, scal_r = Renderer(ref_elem, temp_elem, half, defs), Renderer(ref_scalar, temp_scalar, half, defs)
     deps = dependencies(sm.steps)
     needed = deps[online.max_step.name]
     by_name = {s.name: s for s in sm.steps}

@@ -370,3 +370,22 @@ def test_mask_words_load_at_the_widest_aligned_width(off, form, tk):
         if wider == form:
             break
         assert f"const {wider} w_" not in body
+
+
+def test_shifted_fast_exp_only_for_the_row_max():
+    """``exp_fast_shift`` folds the rounding of ``m log2 e`` into a factor the
+    normalisation cancels, which holds only when ``m`` is the row's maximum
+    (an ``x - rowmax(x)`` of ``nonpositive_args``); the exp of any other
+    difference is ``exp_fast`` of the rounded difference."""
+    from mlc.codegen.hip_attention import _FastExpRenderer
+    from mlc.ir.scalar import Call, Load
+
+    diff = Call("sub", (Load(0), Load(1)))
+    e = Call("exp", (diff,))
+
+    def render(nonpos):
+        r = _FastExpRenderer(lambda s: (f"x{s}", "float"), lambda n: (n, "float"), nonpos=nonpos)
+        return r(e)[0]
+
+    assert render(frozenset()) == "mlc::exp_fast((x0 - x1))"
+    assert render(frozenset({diff})) == "mlc::exp_fast_shift(x0, x1)"
