@@ -69,9 +69,15 @@ def load_type(dtype: torch.dtype) -> VType:
 
 @lru_cache(maxsize=None)
 def call_type(fn: str, args: tuple[VType, ...]) -> VType:
-    """Result type of scalar function ``fn`` over operands of these types."""
+    """Result type of scalar function ``fn`` over operands of these types. A
+    combination torch itself refuses (the negation of a boolean, say) is
+    typed fp32, which rounds nothing: the register code decides its value."""
     ts = [torch.empty((1,) if dim else (), dtype=dt, device="meta") for dt, dim in args]
-    return _TORCH_FN[fn](*ts).dtype, any(dim for _, dim in args)
+    dims = any(dim for _, dim in args)
+    try:
+        return _TORCH_FN[fn](*ts).dtype, dims
+    except (RuntimeError, TypeError, NotImplementedError):
+        return torch.float32, dims
 
 
 def expr_type(e: Expr, inputs: Callable[[int], VType], temps: Callable[[str], VType],

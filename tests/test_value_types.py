@@ -88,6 +88,8 @@ def test_known_answers():
     assert _t(Call("add", (Const(1.0, F16), Const(2.0, F16)))) == (F16, False)
     assert _t(Const(False)) == (B, True)
     assert call_type("sigmoid", ((BF16, True),)) == (BF16, True)
+    # what torch refuses is typed fp32 (no rounding), not an error
+    assert call_type("neg", ((B, True),)) == (F32, True)
 
 
 def test_reductions_keep_their_operand_type():
