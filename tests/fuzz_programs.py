@@ -107,7 +107,10 @@ class Chain:
         #: every dtype a value of the chain is stored in
         self.dtypes = {dtype}
         reduced = False
+        normalised = False
+        int_prefix = False
         if rng.random() < 0.15:
+            int_prefix = True
             # an integer prefix: int64 arithmetic, comparisons to bool, back to fp32
             self.ops.append(("unary",) + _TO_INT)
             for _ in range(rng.randint(1, 3)):
@@ -170,6 +173,16 @@ class Chain:
                 # into a unit: keep those rows wide
                 if (r == "layer_norm" and cur[d] < 16) or (r == "var" and cur[d] < 4):
                     r = "sum"
+                # a row of an integer prefix's few values may be one value
+                # repeated, which a LayerNorm maps to 0 plus its mean's rounding
+                # times 1/sqrt(eps); and a LayerNorm's row sums to 0 exactly,
+                # so a later sum or mean is all cancellation. Both measure
+                # rounding noise, not the kernels
+                if r == "layer_norm" and int_prefix:
+                    r = "softmax"
+                if r in ("sum", "mean", "var") and normalised:
+                    r = "amax"
+                normalised |= r == "layer_norm"
                 keep = rng.random() < 0.5
                 self.ops.append(("reduce", r, d, keep))
                 if r not in ("softmax", "layer_norm"):
