@@ -89,9 +89,10 @@ def test_fp16_models_against_reference_outputs(key):
     reference torch backend's own outputs (``tests/golden/
     reference_outputs_fp16.npz``, written by the reference compiler on the
     CPU): max error relative to the reference's largest magnitude within the
-    fp16 bar (2e-3; 3e-3 for BERT's pooled output, the named exception of
-    ``FP16_EXCEPTIONS``). For GPT-2 the fixture holds a sample of the logits
-    (every 101st at b1, every 10007th at b32 s512) and each row's maximum."""
+    fp16 bar of 2e-3, BERT b1's pooled output included (1.78e-3); BERT b32's
+    pooled output keeps the exception of ``FP16_EXCEPTIONS`` (2.61e-3). For
+    GPT-2 the fixture holds a sample of the logits (every 101st at b1, every
+    10007th at b32 s512) and each row's maximum."""
     import pathlib
 
     import numpy as np
@@ -102,7 +103,7 @@ def test_fp16_models_against_reference_outputs(key):
     out = mlc.compile(model, args)(*args)
     out = (out if isinstance(out, torch.Tensor) else out[0]).detach()
     torch.cuda.synchronize()
-    bar = FP16_EXCEPTIONS.get(key, FP16_BAR)
+    bar = 3e-3 if key == "C4" else FP16_BAR
     assert list(out.shape) == ref[f"{key}_shape"].tolist()
     if key in ("C3", "C5"):
         step = 101 if key == "C3" else 10007
