@@ -58,3 +58,24 @@ def test_counter_bytes_are_scaled_by_the_plain_copy():
 def test_counter_bytes_need_the_copy():
     with pytest.raises(SystemExit, match="1 GiB copy"):
         _counter_bytes([{"Kernel_Name": "mlc_x", "Counter_Value": "1"}])
+
+
+def test_producer_split_groups_by_the_kernel_that_wrote_the_input(tmp_path):
+    import csv
+
+    from mlc.bench.producer import split
+
+    gemm = "Cijk_Alik_Bljk_HHS_BH_MT64x64x32"
+    copy = "void at::native::elementwise_kernel<128, 4, direct_copy_kernel_cuda>"
+    rows = [_row(gemm, 0, 10_000), _row("mlc_s", 12_000, 19_000),     # after bmm: 7 us, gap 2
+            _row(copy, 20_000, 23_000), _row("mlc_s", 24_000, 30_000),  # after copy: 6 us, gap 1
+            _row("mlc_s", 31_000, 36_000)]                              # after itself: 5 us
+    with open(tmp_path / "t_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    text = split(str(tmp_path), None)
+    assert text.startswith("`mlc_s`")
+    assert "| after the library bmm | 1 | 7.00 | 7.00 | 2.00 |" in text
+    assert "| after a torch copy | 1 | 6.00 | 6.00 | 1.00 |" in text
+    assert "| after itself | 1 | 5.00 | 5.00 | 1.00 |" in text
