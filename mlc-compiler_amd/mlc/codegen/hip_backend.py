@@ -255,6 +255,15 @@ class Renderer:
     def _call(self, e: Call) -> tuple[str, str]:
         plain, self._plain = self._plain, False
         args = [self(a) for a in e.args]
+        if e.fn in ("add", "sub"):
+            nt = self.value_type(e)
+            if nt is not None and nt[0] in ROUND:
+                # torch's CPU add and sub of an fp16/bf16 tensor and a 0-dim
+                # constant first convert the constant to that type (its mul
+                # and div use the constant's fp32 value)
+                args = [(float_literal(_round_half(float(x.value), nt[0])), "float")
+                        if isinstance(x, Const) and not isinstance(x.value, bool) else arg
+                        for x, arg in zip(e.args, args)]
         codes = [c for c, _ in args]
         types = [t for _, t in args]
         top = max(types, key=lambda t: _RANK[t]) if types else "float"

@@ -20,7 +20,9 @@ The reference evaluates a kernel body with torch ops over whole tensors
 ``kernel_types`` types every temporary of a kernel that way; the HIP renderer
 keeps fp32 registers throughout and rounds a narrow-typed result to its type
 (one fp32 operation then one rounding, which is how torch's CPU kernels
-evaluate fp16 and bf16 arithmetic).
+evaluate fp16 and bf16 arithmetic; their add and sub convert a 0-dim
+constant to the narrow type first, their mul and div use its fp32 value, and
+the renderer does the same).
 """
 
 from __future__ import annotations

@@ -233,6 +233,39 @@ def test_negation_of_bf16_values_is_exact():
         assert torch.equal(g[ok].view(torch.int16), w[ok].view(torch.int16)), f"output {i}: bits"
 
 
+class _NarrowChain(torch.nn.Module):
+    """Arithmetic after casts to fp16 and bf16, which the reference's torch
+    evaluation does in the narrow type, rounding every result."""
+
+    def forward(self, x, y):
+        h, b = x.half(), y.bfloat16()
+        p = (h * 3.0 + h.abs()) / 7.0 - 0.1
+        q = torch.maximum(b * b - 2.0, b / 3.0)
+        return p, q, torch.where(p > 0, p, p * 0.5), (h * h).sum(dim=-1)
+
+
+def test_narrow_arithmetic_matches_the_oracle_bit_for_bit():
+    """Each add, mul, division by a constant and comparison after a cast to
+    fp16 or bf16 is one fp32 operation rounded to the narrow type, as torch's
+    kernels evaluate it, so the HIP path equals the oracle bit for bit; the
+    fp16 row sum accumulates in fp32 and rounds once (equal to the oracle's
+    within one fp16 ulp, the two summing in different orders)."""
+    from oracle import compile_reference
+
+    torch.manual_seed(0)
+    x, y = torch.randn(64, 96) * 4, torch.randn(64, 96) * 4
+    cfg = Config(cuda_graphs=False)
+    want = compile_reference(_NarrowChain(), (x, y), cfg)(x, y)
+    got = mlc.compile(_NarrowChain(), (x.cuda(), y.cuda()), cfg)(x.cuda(), y.cuda())
+    torch.cuda.synchronize()
+    for i, (g, w) in enumerate(zip(got[:3], want[:3])):
+        g = g.cpu()
+        assert g.dtype == w.dtype and torch.equal(g.view(torch.int16), w.view(torch.int16)), i
+    g, w = got[3].cpu().double(), want[3].double()
+    ulp = torch.finfo(torch.float16).eps * w.abs().clamp_min(2 ** -14)
+    assert got[3].dtype == torch.float16 and bool(((g - w).abs() <= ulp).all())
+
+
 class _ShiftedExp(torch.nn.Module):
     def forward(self, x):
         return torch.exp(x - x.amax(dim=-1, keepdim=True))

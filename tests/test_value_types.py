@@ -122,6 +122,24 @@ def test_narrow_arithmetic_is_rounded_in_the_generated_code():
     assert "mlc::round_f16(mlc::row_reduce<" in src
 
 
+class _NarrowConstants(torch.nn.Module):
+    def forward(self, x):
+        h = x.half()
+        return h - 0.1, h * 0.1
+
+
+def test_narrow_add_rounds_its_constant_and_mul_does_not():
+    """torch's CPU kernels add an fp16 tensor and a constant in fp16 (the
+    constant converted first) but multiply by the constant's fp32 value."""
+    args = (torch.randn(4, 64),)
+    cfg = Config(cuda_graphs=False)
+    src = build_module(build_pipeline(capture(_NarrowConstants(), args), cfg), cfg).source
+    lines = [ln for ln in src.splitlines() if "0x1.99" in ln]
+    assert len(lines) == 2
+    assert any("0x1.9980000000000p-4f" in ln and "neg_one_" in ln for ln in lines)  # fp16(0.1)
+    assert any("0x1.99999a0000000p-4f" in ln and "neg_zero_" in ln for ln in lines)  # fp32(0.1)
+
+
 @pytest.mark.parametrize("key", ["C1", "C2", "C3", "C4"])
 def test_benchmark_kernels_have_no_narrow_arithmetic(key):
     """The BASELINE models cast to fp16 only right before a store: none of
