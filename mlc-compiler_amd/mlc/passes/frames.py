@@ -187,10 +187,17 @@ def row_constant_layout(v: Value, frame: Frame) -> Layout:
     reshape of the row shape (same count, e.g. ``[1, 100]`` against rows
     ``(100,)``) is read through the reshape."""
     shape = tuple(v.shape)
+    lay = v.layout
+    # leading size-1 dims beyond the row's rank only align the operand with
+    # a reshaped row shape (a [1, 1] scalar read at [1, R] for rows (R,));
+    # broadcasting ignores them
+    extra = len(shape) - len(frame.row)
+    if extra > 0 and all(d == 1 for d in shape[:extra]):
+        lay, shape = lay.squeeze(range(extra)), shape[extra:]
     if shape == frame.row:
-        lay = v.layout
+        pass
     elif _broadcasts(shape, frame.row):
-        lay = v.layout.expand(frame.row)
+        lay = lay.expand(frame.row)
     else:
         lay = v.layout.reshape(frame.row)
         if lay is None:

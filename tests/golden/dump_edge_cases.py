@@ -6,7 +6,8 @@ Each case is a small program at the edge of the reduction-fusion frame rules:
 a row output that reads a row-constant operand, a reshape of the row shape,
 shapes that right-align onto the element shape (among them a LayerNorm whose
 batch is 1 and whose rows are as long as the sequence), a permutation that
-passes the reshape test, and zero-element inputs (no rows, or rows of no
+passes the reshape test, a [1, 1] scalar added before a transpose makes its
+row shape a reshape, and zero-element inputs (no rows, or rows of no
 columns). Per case the fixture records what the reference does:
 the exception it raises (type and message), or its schedule (kernel
 summaries, operand buffers and index strings) and whether its torch backend's
@@ -55,6 +56,10 @@ def cases():
         def forward(self, x):
             return F.layer_norm(x, (x.shape[-1],))
 
+    class ScalarOperandTransposedRow(torch.nn.Module):
+        def forward(self, x, y):
+            return (torch.relu(x) + y).transpose(0, 1).sum(dim=1, keepdim=True)
+
     class AffineRelu(torch.nn.Module):
         def forward(self, x):
             return torch.relu(x * 2.0 + 1.0)
@@ -82,6 +87,7 @@ def cases():
         ("permuted_row_value", PermutedRowValue(), (rn(16, 3, 64, 5), rn(3, 64, 1))),
         ("layer_norm_row_matches_trailing", LayerNormRowMatchesTrailing(), (rn(1, 128, 128),)),
         ("layer_norm_b2", LayerNormRowMatchesTrailing(), (rn(2, 128, 128),)),
+        ("scalar_operand_transposed_row", ScalarOperandTransposedRow(), (rn(1, 100), rn(1, 1))),
         # zero-element inputs: no rows, or rows of no columns
         ("empty_rows_pointwise", AffineRelu(), (rn(0, 16),)),
         ("empty_rows_softmax", Softmax(), (rn(0, 16),)),

@@ -95,7 +95,8 @@ def test_edge_case_row_output_reading_an_operand():
     torch.testing.assert_close(got, model(*args), rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("name", ["reshaped_row_operand", "permuted_row_value"])
+@pytest.mark.parametrize("name", ["reshaped_row_operand", "permuted_row_value",
+                                  "scalar_operand_transposed_row"])
 def test_edge_cases_the_reference_cannot_lower(name):
     """The reference raises ValueError while lowering these (recorded); here
     they compile and match eager."""
@@ -235,7 +236,8 @@ def test_random_programs_hip_matches_oracle(seed, cname):
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["row_output_reads_operand", "reshaped_row_operand",
                                   "permuted_element_producer", "permuted_row_value",
-                                  "right_aligned_row_result", "layer_norm_row_matches_trailing"])
+                                  "right_aligned_row_result", "layer_norm_row_matches_trailing",
+                                  "scalar_operand_transposed_row"])
 def test_edge_cases_hip_matches_oracle(name):
     import mlc
 
