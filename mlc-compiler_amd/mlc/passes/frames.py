@@ -182,12 +182,24 @@ def storable_value(v: Value, frame: Frame) -> bool:
 # layouts over (row, col)
 # --------------------------------------------------------------------------
 
-def row_constant_layout(v: Value, frame: Frame) -> Layout:
+def _without_ones(shape) -> tuple[int, ...]:
+    return tuple(d for d in shape if d != 1)
+
+
+def row_constant_layout(v: Value, frame: Frame, target=None) -> Layout:
     """A row-shaped value spread over the columns with stride 0. A row-major
     reshape of the row shape (same count, e.g. ``[1, 100]`` against rows
-    ``(100,)``) is read through the reshape."""
+    ``(100,)``) is read through the reshape. Read in a node whose output
+    ``target`` is the row shape with size-1 dims added or dropped (a keepdim
+    row value whose 1 a view moved: ``[3, 1, 4099]`` for rows ``(3, 4099)``),
+    the operand broadcasts against ``target`` first, as torch aligns it."""
     shape = tuple(v.shape)
     lay = v.layout
+    if target is not None:
+        target = tuple(target)
+        if (target != frame.row and _without_ones(target) == _without_ones(frame.row)
+                and shape != target and _broadcasts(shape, target)):
+            lay, shape = lay.expand(target), target
     # leading size-1 dims beyond the row's rank only align the operand with
     # a reshaped row shape (a [1, 1] scalar read at [1, R] for rows (R,));
     # broadcasting ignores them
@@ -199,7 +211,7 @@ def row_constant_layout(v: Value, frame: Frame) -> Layout:
     elif _broadcasts(shape, frame.row):
         lay = lay.expand(frame.row)
     else:
-        lay = v.layout.reshape(frame.row)
+        lay = lay.reshape(frame.row)
         if lay is None:
             raise ReductionLoweringError(f"{v.name}{list(shape)} neither broadcasts to nor views "
                                          f"the row shape {list(frame.row)}")
@@ -215,7 +227,7 @@ def frame_layout(v: Value, target, frame: Frame) -> tuple[list, Layout]:
         return frame.split(), lay.permute(frame.order)
     axes = frame_axes(target, frame)
     if axes[0][1] == frame.row:
-        return frame.split(), row_constant_layout(v, frame)
+        return frame.split(), row_constant_layout(v, frame, target)
     # a reshaped element shape, indexed in its own equivalent split
     return axes, v.layout if tuple(v.shape) == target else v.layout.expand(target)
 

@@ -7,7 +7,8 @@ a row output that reads a row-constant operand, a reshape of the row shape,
 shapes that right-align onto the element shape (among them a LayerNorm whose
 batch is 1 and whose rows are as long as the sequence), a permutation that
 passes the reshape test, a [1, 1] scalar added before a transpose makes its
-row shape a reshape, and zero-element inputs (no rows, or rows of no
+row shape a reshape, an operand broadcast against a keepdim row value whose
+size-1 dim a view moved, and zero-element inputs (no rows, or rows of no
 columns). Per case the fixture records what the reference does:
 the exception it raises (type and message), or its schedule (kernel
 summaries, operand buffers and index strings) and whether its torch backend's
@@ -60,6 +61,10 @@ def cases():
         def forward(self, x, y):
             return (torch.relu(x) + y).transpose(0, 1).sum(dim=1, keepdim=True)
 
+    class MovedKeepdimRow(torch.nn.Module):
+        def forward(self, x, y):
+            return torch.reciprocal(x.sum(dim=2, keepdim=True).transpose(2, 1).abs() + 1.0) - y
+
     class AffineRelu(torch.nn.Module):
         def forward(self, x):
             return torch.relu(x * 2.0 + 1.0)
@@ -88,6 +93,7 @@ def cases():
         ("layer_norm_row_matches_trailing", LayerNormRowMatchesTrailing(), (rn(1, 128, 128),)),
         ("layer_norm_b2", LayerNormRowMatchesTrailing(), (rn(2, 128, 128),)),
         ("scalar_operand_transposed_row", ScalarOperandTransposedRow(), (rn(1, 100), rn(1, 1))),
+        ("moved_keepdim_row", MovedKeepdimRow(), (rn(3, 50, 4), rn(3, 1, 1))),
         # zero-element inputs: no rows, or rows of no columns
         ("empty_rows_pointwise", AffineRelu(), (rn(0, 16),)),
         ("empty_rows_softmax", Softmax(), (rn(0, 16),)),

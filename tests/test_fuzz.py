@@ -96,7 +96,7 @@ def test_edge_case_row_output_reading_an_operand():
 
 
 @pytest.mark.parametrize("name", ["reshaped_row_operand", "permuted_row_value",
-                                  "scalar_operand_transposed_row"])
+                                  "scalar_operand_transposed_row", "moved_keepdim_row"])
 def test_edge_cases_the_reference_cannot_lower(name):
     """The reference raises ValueError while lowering these (recorded); here
     they compile and match eager."""
@@ -237,7 +237,7 @@ def test_random_programs_hip_matches_oracle(seed, cname):
 @pytest.mark.parametrize("name", ["row_output_reads_operand", "reshaped_row_operand",
                                   "permuted_element_producer", "permuted_row_value",
                                   "right_aligned_row_result", "layer_norm_row_matches_trailing",
-                                  "scalar_operand_transposed_row"])
+                                  "scalar_operand_transposed_row", "moved_keepdim_row"])
 def test_edge_cases_hip_matches_oracle(name):
     import mlc
 
