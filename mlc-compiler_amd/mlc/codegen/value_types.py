@@ -35,8 +35,6 @@ import torch
 from ..ir.scalar import Call, Cast, Const, Expr, Load, Ref
 from ..kernels import Bind, PointwiseKernel, Reduce, ReductionKernel
 
-NARROW = (torch.float16, torch.bfloat16)
-
 #: torch type of a value and whether it has dimensions (a 0-dim constant
 #: does not, and so does not decide the result type of a call against a
 #: dimensioned operand of the same category)
@@ -56,10 +54,6 @@ _TORCH_FN: dict[str, Callable] = {
     "ne": torch.ne, "logical_and": torch.logical_and, "logical_or": torch.logical_or,
     "where": torch.where,
 }
-
-#: calls whose result is one of their operands' values, or its exact
-#: negation or floor: no rounding, in any type
-EXACT_CALLS = frozenset({"maximum", "minimum", "where", "neg", "abs", "floor"})
 
 _BUFFER = {torch.float16: torch.float32, torch.bfloat16: torch.float32}
 
@@ -142,8 +136,5 @@ def kernel_types(k, online: frozenset[str] = frozenset()) -> dict[str, VType]:
     return types
 
 
-def narrow(t: VType) -> torch.dtype | None:
-    return t[0] if t[0] in NARROW else None
-
-
+#: the narrow types, each with the device function that rounds an fp32 value to it
 ROUND = {torch.float16: "mlc::round_f16", torch.bfloat16: "mlc::round_bf16"}
