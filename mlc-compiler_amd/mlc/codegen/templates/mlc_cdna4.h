@@ -34,8 +34,16 @@ struct bf16 {
   uint16_t bits;
 };
 
+// The widened value passes through an empty inline-assembly statement (no
+// instruction): ROCm 7.2's instruction selector, with packed fp32 off, folds
+// a negation of such a value into the shift when two of them pair into a
+// v2f32 operation, and then either aborts ("Cannot select: v2f32 = bitcast")
+// or drops the sign of one lane (exp(x) for exp(-x) in a sigmoid). An opaque
+// fp32 value is negated like any other.
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
-  return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+  float f = __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+  asm("" : "+v"(f));
+  return f;
 }
 
 // Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).

@@ -179,13 +179,15 @@ def test_no_packed_fp32_by_hand_and_no_scalar_stores():
     text = src + native.TEMPLATES.joinpath("mlc_cdna4.h").read_text()
     assert not re.search(r"v_pk_(add|mul|fma)_f32", text)
     assert "-packed-fp32-ops" in native.HIP_FLAGS
-    # two inline asm statements: an empty template that only hides a constant
-    # in an SGPR from the optimiser (it emits no instruction), and fp32
-    # negation as one vector-register xor
+    # three inline asm statements: two empty templates that only hide a value
+    # from the optimiser (a constant in an SGPR; a value widened from bf16 in
+    # a VGPR), which emit no instruction, and fp32 negation as one
+    # vector-register xor
     opaque = 'asm("" : "+s"(v));'
+    widened = 'asm("" : "+v"(f));'
     neg = 'asm("v_xor_b32 %0, 0x80000000, %1" : "=v"(r) : "v"(x));'
-    assert text.count(opaque) == 1 and text.count(neg) == 1
-    assert "asm" not in text.replace(opaque, "").replace(neg, "")
+    assert text.count(opaque) == 1 and text.count(widened) == 1 and text.count(neg) == 1
+    assert "asm" not in text.replace(opaque, "").replace(widened, "").replace(neg, "")
 
 
 @pytest.mark.parametrize("name,cfg", [("pre_norm_block", FULL), ("masked_softmax", STREAMED),
@@ -218,6 +220,31 @@ def test_negation_of_bf16_values_cross_compiles(tmp_path, monkeypatch):
     assert "mlc::neg_(" in body and "(-(" not in body
     _, obj = native.compile_code_object(mod.source)
     assert obj.stat().st_size > 0
+
+
+class _SigmoidOfBf16Select(torch.nn.Module):
+    def forward(self, x, y):
+        return torch.sigmoid(torch.where(x > y, x, y))
+
+
+def test_bf16_sigmoid_keeps_its_negation(tmp_path):
+    """With packed fp32 off, ROCm 7.2 folded the negation inside a sigmoid
+    of values widened from bf16 into the widening shift when two lanes of the
+    scalar tail paired up, and dropped the sign of one: its exp multiplied by
+    +log2(e) where every exp(-x) multiplies by -log2(e) (0xbfb8aa3b). The
+    header's widening is opaque to that fold; every exp here keeps the sign."""
+    import subprocess
+
+    args = (torch.randn(10).bfloat16(), torch.randn(10).bfloat16())
+    mod = build_module(build_pipeline(capture(_SigmoidOfBf16Select(), args), FULL), FULL)
+    src = tmp_path / "m.hip"
+    src.write_text(mod.source)
+    asm = tmp_path / "m.s"
+    subprocess.run([native.hipcc(), "--cuda-device-only", "-S", *native.HIP_FLAGS,
+                    f"-I{native.TEMPLATES}", "-x", "hip", str(src), "-o", str(asm)],
+                   check=True, capture_output=True)
+    text = asm.read_text()
+    assert text.count("0xbfb8aa3b") > 0 and "0x3fb8aa3b" not in text
 
 
 def test_copy_ceiling_kernel_cross_compiles(tmp_path, monkeypatch):

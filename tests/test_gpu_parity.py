@@ -233,6 +233,27 @@ def test_negation_of_bf16_values_is_exact():
         assert torch.equal(g[ok].view(torch.int16), w[ok].view(torch.int16)), f"output {i}: bits"
 
 
+class _SigmoidOfBf16Select(torch.nn.Module):
+    def forward(self, x, y):
+        return torch.sigmoid(torch.where(x > y, x, y))
+
+
+@pytest.mark.parametrize("n", [10, 13, 4099])
+def test_bf16_sigmoid_in_the_scalar_tail(n):
+    """A sigmoid of a select of bf16 values over counts that leave a scalar
+    tail (ROCm 7.2 once dropped the negation of one paired tail lane, giving
+    sigmoid(-x)): every element within one bf16 rounding of fp32 on the CPU."""
+    torch.manual_seed(0)
+    x, y = torch.randn(n).bfloat16() * 3, torch.randn(n).bfloat16() * 3
+    want = torch.sigmoid(torch.where(x > y, x, y).float())
+    got = mlc.compile(_SigmoidOfBf16Select(), (x.cuda(), y.cuda()),
+                      Config(cuda_graphs=False))(x.cuda(), y.cuda())
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16
+    err = (got.cpu().float() - want).abs() / want.abs()
+    assert bool((err <= 2.0 ** -8).all()), err.max().item()
+
+
 class _NarrowChain(torch.nn.Module):
     """Arithmetic after casts to fp16 and bf16, which the reference's torch
     evaluation does in the narrow type, rounding every result."""
