@@ -196,13 +196,15 @@ def test_empty_inputs_on_the_gpu(name, graphs):
     assert torch.equal(got.cpu(), want)
 
 
-#: the last four compute on values cast to fp16/bf16 (arithmetic the reference
-#: does, and rounds, in the narrow type) and normalise long bf16 rows
+#: the last five: four compute on values cast to fp16/bf16 (arithmetic the
+#: reference does, and rounds, in the narrow type) and normalise long bf16
+#: rows; seed 622's wide form takes a sigmoid of a select of bf16 values in a
+#: pointwise kernel's scalar tail (where ROCm 7.2 once dropped a negation)
 GPU_CASES = [(s, "default") for s in range(16)] + [(s, "streamed") for s in range(6)] + \
     [(s, "layout") for s in range(4)] + [(s, "wide") for s in range(6)] + \
     [(s, "wide_streamed") for s in range(3)] + [(s, "no_fusion") for s in range(2)] + \
     [(s, "elementwise") for s in range(2)] + [(s, "unplanned") for s in range(2)] + \
-    [(124, "default"), (133, "default"), (118, "wide"), (145, "wide")]
+    [(124, "default"), (133, "default"), (118, "wide"), (145, "wide"), (622, "wide")]
 GPU_CONFIGS = {"default": CFG, "streamed": Config(cuda_graphs=False, max_persistent_row=16),
                "layout": Config(cuda_graphs=False, layout_selection=True), "wide": CFG,
                "wide_streamed": Config(cuda_graphs=False, max_persistent_row=512),
